@@ -1,0 +1,153 @@
+/*
+ * tkmi.h -- C ABI of libtkmi.so, the MI355X (gfx950) kernels of the
+ * transformer-layer forward path.
+ *
+ * Conventions
+ *   - Every entry point is extern "C", returns int: 0 on success, a negative
+ *     TK_ERR_* code on a rejected argument, or TK_ERR_HIP when the HIP runtime
+ *     reported an error at launch.  tk_last_error_string() describes the last
+ *     failure on the calling thread.
+ *   - All buffers are DEVICE pointers owned by the caller (the Python side
+ *     allocates them with torch.empty).  No entry point allocates device or
+ *     host memory, none synchronizes; each enqueues on `stream` (a
+ *     hipStream_t passed as void*; NULL = the legacy default stream).
+ *   - tk_half is IEEE binary16 storage.  Row-major layouts; leading
+ *     dimensions (ld*) and strides are in ELEMENTS.
+ *
+ * The reference (danielfodgaard/transformer-kernel) exposes this path as
+ * Python functions on torch tensors; each entry point below names the
+ * reference interface it replaces (paths relative to the reference repo).
+ */
+#ifndef TKMI_H
+#define TKMI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TKMI_ABI_VERSION 1
+
+typedef uint16_t tk_half;
+
+enum tk_status {
+  TK_OK = 0,
+  TK_ERR_ARG = -1,         /* null pointer, bad size, bad stride, bad enum */
+  TK_ERR_UNSUPPORTED = -2, /* valid request outside the kernels' envelope  */
+  TK_ERR_HIP = -3          /* the HIP runtime rejected the launch          */
+};
+
+enum tk_dtype { TK_F32 = 0, TK_F16 = 1 };
+
+enum tk_epilogue {
+  TK_EPI_BIAS = 0,      /* C(f16)  = A.W^T + bias                          */
+  TK_EPI_BIAS_GELU = 1, /* C(f16)  = gelu_erf(A.W^T + bias)                */
+  TK_EPI_BIAS_RESID = 2 /* C(f32)  = resid + (A.W^T + bias); C may alias resid */
+};
+
+/* ABI version (TKMI_ABI_VERSION) of the loaded library. */
+int tk_version(void);
+
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char *tk_last_error_string(void);
+
+/*
+ * LayerNorm over the last dim + cast.
+ *   out[r, :] = (x[r,:] - mean) * rsqrt(var_pop + eps) * w + b   (fp32 math)
+ * x: [rows, cols] f32 contiguous; w, b: [cols] f32; out: [rows, cols] of
+ * out_dtype (TK_F16 or TK_F32).  cols in [1, 8192].
+ * Replaces fused_kernels.ln_fwd / _ln_kernel (src/fused_kernels.py:164-193,
+ * :80-112).
+ */
+int tk_ln_cast(const float *x, const float *w, const float *b, void *out,
+               int out_dtype, int64_t rows, int64_t cols, float eps,
+               void *stream);
+
+/*
+ * Residual add + LayerNorm + cast.
+ *   s = x + y (fp32);  h = LN(s) cast to h_dtype.
+ * y has y_dtype (TK_F16 or TK_F32).  sum_out may be NULL (s not stored) and
+ * may alias x.  cols in [1, 8192].
+ * Replaces fused_kernels.add_ln_fwd / _add_ln_kernel
+ * (src/fused_kernels.py:196-238, :114-161).
+ */
+int tk_add_ln_cast(const float *x, const void *y, int y_dtype, const float *w,
+                   const float *b, float *sum_out, void *h_out, int h_dtype,
+                   int64_t rows, int64_t cols, float eps, void *stream);
+
+/*
+ * GEMM  C[m, n] = epilogue( sum_k A[m, k] * W[n, k] + bias[n] )
+ * A: [m, k] f16 (lda), W: [n, k] f16 (ldw) -- the nn.Linear weight layout,
+ * bias: [n] f32 (may be NULL = 0), fp32 accumulation on MFMA.
+ * epilogue TK_EPI_BIAS / TK_EPI_BIAS_GELU: C is f16 (ldc).
+ * epilogue TK_EPI_BIAS_RESID: C is f32 (ldc), resid is f32 (ldr), C may
+ * equal resid (in-place residual stream update).
+ * k must be a multiple of 8 and lda/ldw multiples of 8 (16-byte rows).
+ * Replaces torch F.linear (+ F.gelu) in src/optimized.py:572,627,632-636.
+ */
+int tk_gemm(const tk_half *a, int64_t lda, const tk_half *w, int64_t ldw,
+            const float *bias, const float *resid, int64_t ldr, void *c,
+            int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
+            void *stream);
+
+/*
+ * GEMM with the residual + LayerNorm + cast epilogue over full output rows:
+ *   s = resid + A.W^T + bias (fp32);  h = LN(s; ln_w, ln_b, eps) -> h_dtype
+ * sum_out (may be NULL, may alias resid) receives s.  Rows of n elements
+ * must fit one tile: n in {128, 256, 512} (tk_gemm_ln_supported).
+ * Replaces F.linear followed by fused_kernels.add_ln_fwd
+ * (src/optimized.py:523-553 with :627 / :636).
+ */
+int tk_gemm_bias_add_ln(const tk_half *a, int64_t lda, const tk_half *w,
+                        int64_t ldw, const float *bias, const float *resid,
+                        const float *ln_w, const float *ln_b, float *sum_out,
+                        void *h_out, int h_dtype, int64_t m, int64_t n,
+                        int64_t k, float eps, void *stream);
+
+/* 1 when tk_gemm_bias_add_ln handles rows of n elements, else 0. */
+int tk_gemm_ln_supported(int64_t n);
+
+/*
+ * FlashAttention-2-style forward (online softmax, scores never stored).
+ * q, k, v: logical [batch, heads, seq, head_dim] f16 with element strides
+ * {b, h, s} given in *_strides[3] (head_dim stride is 1).  out: logical
+ * [batch, heads, seq, head_dim] written through o_strides (pass
+ * {S*H*hd, hd, H*hd} for the [B, S, H*hd] layout).
+ * scores = (q.k^T) * scale in fp32, causal masks key > query, fp32 softmax,
+ * fp16 P on MFMA for P.V, fp32 accumulation.
+ * head_dim in {16, 32, 64, 128} (tk_attention_supported).
+ * Replaces kernels.flash_attention / _flash_attn_fwd_kernel
+ * (src/kernels.py:250-294, :137-247) and F.scaled_dot_product_attention
+ * (src/optimized.py:615-626).
+ */
+int tk_flash_attn_fwd(const tk_half *q, const tk_half *k, const tk_half *v,
+                      tk_half *out, int64_t batch, int64_t heads, int64_t seq,
+                      int64_t head_dim, const int64_t *q_strides,
+                      const int64_t *k_strides, const int64_t *v_strides,
+                      const int64_t *o_strides, float scale, int causal,
+                      void *stream);
+
+/* 1 when tk_flash_attn_fwd handles head_dim, else 0.
+ * Replaces kernels.attention_supported (src/kernels.py:96-103). */
+int tk_attention_supported(int64_t head_dim);
+
+/*
+ * Masked softmax over rows of materialised scores.
+ * scores: [groups, seq, seq] f32 (query-major, one group per (b, h));
+ * probs: same shape, f16.  causal masks key > query with -inf before the
+ * fp32 softmax; key_len (may be NULL) gives per-batch valid key counts
+ * (group g belongs to batch g / heads_per_batch) -- keys >= key_len masked.
+ * A row whose keys are all masked yields zeros.
+ * Replaces the masked softmax of the baseline attention
+ * (src/torch_transformer_benchmark.py:99-111; src/optimized.py:658-666).
+ */
+int tk_masked_softmax(const float *scores, tk_half *probs, int64_t groups,
+                      int64_t seq, int causal, const int32_t *key_len,
+                      int64_t heads_per_batch, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TKMI_H */

@@ -1,0 +1,277 @@
+"""Per-kernel parity on the GPU: libtkmi vs the CPU oracle on the same seeded inputs.
+
+Test matrices follow the reference's own kernel tests:
+  * LayerNorm: dims [32, 64, 100, 128, 1024] x residual {none, fp16, fp32}, 48 rows,
+    fp32 sum bit-exact, fp16 output within atol 2e-3 / rtol 2e-2
+    (src/test_triton_kernels.py:62-117); widths (32, 128, 1024, 33, 100, 768,
+    2048) x 257 rows, fp32 out 1e-5, fp16 out 1e-3, sum 1e-6
+    (src/test_kernels.py:54-93);
+  * attention: ATTN_SHAPES x {causal, full}, strided q/k/v views of the fused
+    projection, the [B, S, H*hd] output layout, ragged S in {32, 33, 64, 100}
+    (src/test_triton_kernels.py:144-225), at atol 2e-3 / rtol 2e-2.
+GEMM tolerances are stated per test: fp32 accumulation on both sides, so the
+only difference is accumulation order (~1e-6 rel) plus the fp16 output cast
+(<= 2^-11 rel).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import or_rule_violations, seeded
+from oracle import baseline as ob
+
+import tkmi
+from tkmi import _lib, ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+# --------------------------------------------------------------------------- #
+# LayerNorm
+# --------------------------------------------------------------------------- #
+
+
+@pytest.mark.parametrize("d", [32, 64, 100, 128, 1024])
+@pytest.mark.parametrize("residual_dtype", [None, torch.float16, torch.float32])
+def test_layernorm_reference_matrix(d, residual_dtype):
+    rows = 48
+    x = seeded(rows, d, seed=d)
+    w = seeded(d, seed=d + 1, scale=0.5) + 1.0
+    b = seeded(d, seed=d + 2, scale=0.5)
+    xg, wg, bg = x.to(DEV), w.to(DEV), b.to(DEV)
+    if residual_dtype is None:
+        y = ops.ln_fwd(xg, wg, bg, 1e-5, out_dtype=torch.float16)
+        expected_sum = x
+    else:
+        r = seeded(rows, d, dtype=residual_dtype, seed=d + 3)
+        expected_sum = x + r.float()
+        s, y = ops.add_ln_fwd(xg, r.to(DEV), wg, bg, 1e-5, out_dtype=torch.float16)
+        assert torch.equal(s.cpu(), expected_sum)  # the fp32 add is one IEEE op: bit-exact
+    ref = ob.layer_norm_ref(expected_sum, w, b, 1e-5, torch.float16)
+    assert y.dtype == torch.float16 and y.shape == x.shape
+    bad, err = or_rule_violations(y, ref, atol=2e-3, rtol=2e-2)
+    assert bad == 0, err
+
+
+def test_layernorm_fp32_out_is_tight():
+    d, rows = 128, 32
+    x, r = seeded(rows, d, seed=7), seeded(rows, d, seed=8)
+    w, b = seeded(d, seed=9) + 1.0, seeded(d, seed=10)
+    _, y = ops.add_ln_fwd(x.to(DEV), r.to(DEV), w.to(DEV), b.to(DEV), 1e-5)
+    ref = ob.layer_norm_ref(x + r, w, b, 1e-5)
+    torch.testing.assert_close(y.cpu(), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_layernorm_three_dim_and_noncontiguous():
+    x = seeded(3, 5, 128, seed=21)
+    r = seeded(3, 5, 128, dtype=torch.float16, seed=22)
+    w, b = seeded(128, seed=23) + 1.0, seeded(128, seed=24)
+    s, y = ops.add_ln_fwd(x.to(DEV), r.to(DEV), w.to(DEV), b.to(DEV), 1e-5)
+    assert y.shape == (3, 5, 128) and s.shape == (3, 5, 128)
+    torch.testing.assert_close(y.cpu(), ob.layer_norm_ref(x + r.float(), w, b), atol=1e-5, rtol=1e-5)
+    x3 = seeded(4, 16, 128, seed=25).transpose(0, 1)
+    got = ops.ln_fwd(x3.to(DEV), w.to(DEV), b.to(DEV), 1e-5, torch.float16)
+    bad, err = or_rule_violations(got, ob.layer_norm_ref(x3, w, b, 1e-5, torch.float16), atol=1e-3, rtol=0)
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("n_cols", [32, 128, 1024, 33, 100, 768, 2048])
+def test_layernorm_script_matrix(n_cols):
+    rows = 257
+    x = seeded(rows, n_cols, seed=n_cols) * 3
+    y = seeded(rows, n_cols, dtype=torch.float16, seed=n_cols + 1)
+    w, b = seeded(n_cols, seed=n_cols + 2), seeded(n_cols, seed=n_cols + 3)
+    xg, yg, wg, bg = x.to(DEV), y.to(DEV), w.to(DEV), b.to(DEV)
+    for out_dtype, atol in ((torch.float32, 1e-5), (torch.float16, 1e-3)):
+        got = ops.ln_fwd(xg, wg, bg, 1e-5, out_dtype)
+        want = ob.layer_norm_ref(x, w, b, 1e-5, out_dtype)
+        assert (got.cpu().float() - want.float()).abs().max() <= atol
+        s, h = ops.add_ln_fwd(xg, yg, wg, bg, 1e-5, out_dtype)
+        sum_want = x + y.float()
+        assert (s.cpu() - sum_want).abs().max() <= 1e-6
+        assert (h.cpu().float() - ob.layer_norm_ref(sum_want, w, b, 1e-5, out_dtype).float()).abs().max() <= atol
+
+
+@pytest.mark.parametrize("cols", [512, 2048, 4096, 8192])
+def test_layernorm_model_widths_no_sum(cols):
+    rows = 300
+    x, y = seeded(rows, cols, seed=1), seeded(rows, cols, seed=2)
+    w, b = seeded(cols, seed=3) + 1, seeded(cols, seed=4)
+    s, h = ops.add_ln_fwd(x.to(DEV), y.to(DEV), w.to(DEV), b.to(DEV), 1e-5, torch.float32, write_sum=False)
+    assert s is None
+    torch.testing.assert_close(h.cpu(), ob.layer_norm_ref(x + y, w, b), atol=1e-5, rtol=1e-5)
+
+
+# --------------------------------------------------------------------------- #
+# GEMM + epilogues
+# --------------------------------------------------------------------------- #
+
+GEMM_SHAPES = [
+    (512, 384, 128),     # C1 QKV (reduced M)
+    (1024, 1536, 512),   # C2 QKV
+    (1024, 512, 2048),   # C2 FFN-down
+    (4096, 4096, 1024),  # large-tile path (256x256 tiles)
+    (4096, 2048, 8192),  # C4 FFN-down (reduced M), long K
+    (1000, 200, 72),     # ragged M, N, K
+    (77, 300, 8),        # tiny K
+    (130, 130, 136),
+]
+
+
+def _gemm_inputs(m, n, k, seed=0):
+    a = seeded(m, k, seed=seed).half()
+    w = (seeded(n, k, seed=seed + 1) / k ** 0.5).half()
+    bias = seeded(n, seed=seed + 2) * 0.1
+    ref = a.float() @ w.float().T + bias
+    return a, w, bias, ref
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+@pytest.mark.parametrize("gelu", [False, True])
+def test_gemm_bias_and_gelu(m, n, k, gelu):
+    a, w, bias, ref = _gemm_inputs(m, n, k)
+    if gelu:
+        ref = ob.gelu_ref(ref)
+    got = ops.linear(a.to(DEV), w.to(DEV), bias.to(DEV), gelu=gelu)
+    # fp16 output: |d| <= 1e-3 + 1e-3*|ref| (cast <= 4.9e-4 rel, accumulation order ~1e-6)
+    torch.testing.assert_close(got.cpu().float(), ref.half().float(), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES[:6])
+def test_gemm_residual_inplace(m, n, k):
+    a, w, bias, ref = _gemm_inputs(m, n, k, seed=3)
+    resid = seeded(m, n, seed=9)
+    rg = resid.to(DEV)
+    out = ops.linear_residual(a.to(DEV), w.to(DEV), bias.to(DEV), rg, out=rg)
+    assert out.data_ptr() == rg.data_ptr()
+    # fp32 output: accumulation-order differences only
+    torch.testing.assert_close(out.cpu(), resid + ref, atol=5e-5, rtol=1e-5)
+
+
+def test_gemm_strided_operand():
+    a, w, bias, ref = _gemm_inputs(256, 128, 64, seed=5)
+    big = torch.zeros(256, 96, dtype=torch.float16)
+    big[:, 16:80] = a
+    view = big.to(DEV)[:, 16:80]
+    got = ops.linear(view, w.to(DEV), bias.to(DEV))
+    torch.testing.assert_close(got.cpu().float(), ref.half().float(), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("n", [128, 256, 512])
+@pytest.mark.parametrize("m", [64, 1000, 4096])
+def test_gemm_add_layernorm_epilogue(m, n):
+    k = 2 * n
+    a, w, bias, acc = _gemm_inputs(m, n, k, seed=n)
+    resid = seeded(m, n, seed=n + 7) * 2
+    lw, lb = seeded(n, seed=n + 8) * 0.3 + 1, seeded(n, seed=n + 9) * 0.3
+    s_ref = resid + acc
+    h_ref = ob.layer_norm_ref(s_ref, lw, lb, 1e-5)
+    rg = resid.to(DEV)
+    h = ops.linear_add_ln(a.to(DEV), w.to(DEV), bias.to(DEV), rg, lw.to(DEV), lb.to(DEV), 1e-5,
+                          torch.float16, sum_out=rg)
+    torch.testing.assert_close(rg.cpu(), s_ref, atol=5e-5, rtol=1e-5)
+    torch.testing.assert_close(h.cpu().float(), h_ref.half().float(), atol=2e-3, rtol=2e-3)
+    h32 = ops.linear_add_ln(a.to(DEV), w.to(DEV), bias.to(DEV), resid.to(DEV), lw.to(DEV), lb.to(DEV),
+                            1e-5, torch.float32)
+    torch.testing.assert_close(h32.cpu(), h_ref, atol=1e-4, rtol=1e-4)
+
+
+# --------------------------------------------------------------------------- #
+# Attention
+# --------------------------------------------------------------------------- #
+
+ATTN_SHAPES = [  # (B, H, S, hd); the reference's shapes with a supported head_dim
+    (2, 4, 128, 32),
+    (1, 1, 64, 128),
+    (2, 4, 96, 32),
+    (1, 2, 128, 64),
+    (1, 4, 32, 16),
+    (8, 16, 512, 64),   # 128-row tile path
+    (1, 2, 1024, 128),
+    (4, 8, 64, 64),     # C2-like: one key tile per head
+]
+
+
+def _qkv(shape, seed=1):
+    return tuple(seeded(*shape, dtype=torch.float16, seed=seed + i) for i in range(3))
+
+
+@pytest.mark.parametrize("shape", ATTN_SHAPES, ids=lambda s: "b{}h{}s{}d{}".format(*s))
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_flash_attention_matches_reference(shape, causal):
+    b, h, s, hd = shape
+    q, k, v = _qkv(shape)
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
+    ref = ob.attention_ref(q, k, v, hd ** -0.5, causal)
+    assert out.shape == (b, s, h * hd)
+    bad, err = or_rule_violations(out, ref, atol=2e-3, rtol=2e-2)
+    assert bad == 0, err
+
+
+def test_flash_attention_strided_qkv_views():
+    b, h, s, hd = 2, 4, 128, 32
+    qkv = seeded(b, s, 3, h, hd, dtype=torch.float16, seed=42)
+    q, k, v = qkv.to(DEV).permute(2, 0, 3, 1, 4).unbind(0)
+    assert not q.is_contiguous()
+    out = ops.flash_attention(q, k, v, hd ** -0.5, causal=True)
+    qc, kc, vc = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    bad, err = or_rule_violations(out, ob.attention_ref(qc, kc, vc, hd ** -0.5, True))
+    assert bad == 0, err
+
+
+def test_flash_attention_output_layout():
+    b, h, s, hd = 1, 2, 64, 64
+    q, k, v = _qkv((b, h, s, hd), seed=5)
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal=True)
+    assert out.stride() == (s * h * hd, h * hd, 1)
+    bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, True))
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("s", [32, 33, 64, 100])
+def test_flash_attention_ragged_sequence_lengths(s):
+    b, h, hd = 1, 2, 32
+    q, k, v = _qkv((b, h, s, hd), seed=s)
+    for causal in (True, False):
+        out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+
+
+def test_attention_support_probes():
+    assert ops.attention_supported(64, torch.float16, DEV)
+    assert not ops.attention_supported(8, torch.float16, DEV)
+    assert not ops.attention_supported(256, torch.float16, DEV)
+    assert not ops.attention_supported(64, torch.float32, DEV)
+    q = torch.zeros(1, 1, 8, 8, dtype=torch.float16, device=DEV)
+    with pytest.raises(_lib.TkError, match="head_dim"):
+        ops.flash_attention(q, q, q, 1.0, True)
+
+
+# --------------------------------------------------------------------------- #
+# Masked softmax
+# --------------------------------------------------------------------------- #
+
+
+@pytest.mark.parametrize("groups,s", [(3, 64), (2, 128), (4, 100), (2, 2048), (1, 5000)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_masked_softmax(groups, s, causal):
+    scores = seeded(groups, s, s, seed=s) * 3
+    got = ops.masked_softmax(scores.to(DEV), causal)
+    want = ob.masked_softmax_ref(scores, causal)
+    assert (got.cpu().float() - want).abs().max() <= 1e-3  # fp16 cast of values in [0, 1]
+
+
+def test_masked_softmax_key_lengths():
+    b, h, s = 3, 2, 40
+    scores = seeded(b * h, s, s, seed=77)
+    key_len = torch.tensor([40, 17, 1], dtype=torch.int32)
+    got = ops.masked_softmax(scores.to(DEV), True, key_len=key_len, heads_per_batch=h)
+    valid = torch.arange(s)[None, :] < key_len[:, None]  # [B, S]
+    want = torch.stack([ob.masked_softmax_ref(scores[g], True, valid[g // h]) for g in range(b * h)])
+    want = torch.nan_to_num(want, nan=0.0)  # all-masked rows -> zeros
+    assert (got.cpu().float() - want).abs().max() <= 1e-3

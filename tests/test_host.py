@@ -1,0 +1,144 @@
+"""Host-side logic and the C ABI surface, on CPU (no kernel launches).
+
+* the drop-in model keeps the baseline's parameter tree, seeded weights and
+  strict-load compatibility (src/torch_transformer_benchmark.py:203-213,690-696);
+* there is no CPU path: a CPU input raises;
+* libtkmi.so loads and exports every entry point declared in include/tkmi.h;
+  argument validation rejects bad calls before touching the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+
+import pytest
+import torch
+
+from conftest import GOLDEN_DIR, REPO
+from oracle import baseline as ob
+
+import tkmi
+from tkmi import _lib
+
+GOLD = json.loads((GOLDEN_DIR / "golden.json").read_text())
+HEADER = (REPO / "include" / "tkmi.h").read_text()
+
+
+def _declared_symbols():
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tk_\w+)\s*\(", HEADER, re.M)))
+
+
+def test_state_dict_keys_and_seeded_weights_match_baseline():
+    cfg = tkmi.TransformerConfig(2, 16, 64, 4, 128, 2, True)
+    torch.manual_seed(1234)
+    opt = tkmi.OptimizedTransformer(cfg)
+    base = ob.build_model(ob.TransformerConfig(**cfg.__dict__), seed=1234)
+    sd_o, sd_b = opt.state_dict(), base.state_dict()
+    assert list(sd_o) == list(sd_b)
+    for k in sd_b:
+        assert torch.equal(sd_o[k], sd_b[k]), k
+
+
+def test_seeded_weights_match_reference_golden_hash():
+    import hashlib
+
+    meta = GOLD["small"]["tiny_causal"]
+    torch.manual_seed(GOLD["seed"])
+    opt = tkmi.OptimizedTransformer(tkmi.TransformerConfig(**meta["config"]))
+    h = hashlib.sha256()
+    for k, v in opt.state_dict().items():
+        h.update(k.encode())
+        h.update(v.numpy().tobytes())
+    assert h.hexdigest() == meta["state_sha256"]
+
+
+def test_strict_weight_copy_and_no_extra_state():
+    cfg = ob.TransformerConfig(1, 8, 32, 2, 48, 1, False)
+    base = ob.build_model(cfg)
+    opt = tkmi.OptimizedTransformer(tkmi.TransformerConfig(**cfg.__dict__))
+    res = ob.copy_model_weights(base, opt, strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    assert len(list(opt.buffers())) == 0
+
+
+def test_forward_on_cpu_raises_no_fallback():
+    cfg = tkmi.TransformerConfig(1, 8, 64, 4, 64, 1, True)
+    opt = tkmi.OptimizedTransformer(cfg).eval()
+    with pytest.raises(RuntimeError, match="HIP kernels only"):
+        opt(torch.randn(1, 8, 64))
+
+
+def test_ops_reject_cpu_tensors():
+    x = torch.randn(4, 64)
+    w = torch.ones(64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        tkmi.ops.ln_fwd(x, w, w, 1e-5)
+    assert not tkmi.ops.can_fuse(x)
+    assert not tkmi.ops.attention_supported(64, torch.float16, "cpu")
+
+
+def test_configure_and_mask_memo():
+    old = tkmi.active_settings()
+    try:
+        s = tkmi.configure(fused_norm=False)
+        assert s.fused_norm is False and tkmi.active_settings() is s
+        model = tkmi.OptimizedTransformer(tkmi.TransformerConfig(2, 4, 32, 2, 32, 1, True))
+        assert model.settings.fused_norm is False
+        dense = torch.ones(2, 4, dtype=torch.bool)
+        padded = dense.clone()
+        padded[1, 3] = False
+        assert model._mask_is_dense(dense) is True
+        assert model._mask_is_dense(padded) is False
+        assert model._mask_is_dense(None) is True
+    finally:
+        tkmi.configure(**old.__dict__)
+
+
+# --------------------------------------------------------------------------- #
+# C ABI
+# --------------------------------------------------------------------------- #
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert set(declared) == set(_lib.SIGNATURES), (declared, sorted(_lib.SIGNATURES))
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.tk_version() == _lib.ABI_VERSION
+
+
+def test_capability_probes():
+    lib = _lib.load()
+    assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256)] == [0, 1, 1, 1, 1, 0]
+    assert [lib.tk_gemm_ln_supported(n) for n in (64, 128, 256, 512, 1024)] == [0, 1, 1, 1, 0]
+
+
+@pytest.mark.parametrize(
+    "fn,args,code",
+    [
+        ("tk_ln_cast", (None, None, None, None, 1, 4, 64, 1e-5, None), _lib.TK_ERR_ARG),
+        ("tk_ln_cast", (8, 8, 8, 8, 1, 4, 9000, 1e-5, None), _lib.TK_ERR_ARG),
+        ("tk_ln_cast", (8, 8, 8, 8, 7, 4, 64, 1e-5, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 12, 16, 12, None, None, 0, 16, 16, 4, 4, 12, 0, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 9, None), _lib.TK_ERR_ARG),
+        ("tk_gemm_bias_add_ln", (16, 16, 16, 16, None, 16, 16, 16, None, 16, 1, 4, 384, 16, 1e-5, None),
+         _lib.TK_ERR_UNSUPPORTED),
+        ("tk_masked_softmax", (None, None, 1, 4, 1, None, 1, None), _lib.TK_ERR_ARG),
+    ],
+)
+def test_argument_validation_without_gpu(fn, args, code):
+    lib = _lib.load()
+    status = getattr(lib, fn)(*args)
+    assert status == code
+    assert lib.tk_last_error_string().decode()
+
+
+def test_flash_rejects_bad_head_dim_without_gpu():
+    lib = _lib.load()
+    st = _lib.strides3((0, 0, 0))
+    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 48, st, st, st, st, 1.0, 1, None)
+    assert status == _lib.TK_ERR_UNSUPPORTED
+    assert "head_dim" in lib.tk_last_error_string().decode()

@@ -1,0 +1,459 @@
+// fp16 x fp16 -> fp32 MFMA GEMMs with fused epilogues, for gfx950.
+//
+//   C[m, n] = epi( sum_k A[m, k] * W[n, k] + bias[n] )
+//
+// A is the activation [M, K] and W the nn.Linear weight [N, K]; both are
+// K-contiguous, which is exactly the operand layout v_mfma_f32_32x32x16_f16
+// wants (each lane feeds 8 consecutive k of one row).  The kernel computes
+// the transposed product C^T = W . A^T on the matrix cores so that every lane
+// ends up holding 4 consecutive n of one output row m: bias, GELU, residual
+// and LayerNorm epilogues then work on 16-byte (fp32) / 8-byte (fp16)
+// vectors along the row.
+//
+// Block tile BM x BN, K-step 64, two LDS stages.  Tiles are stored in LDS as
+// 128-byte rows of eight 16-byte chunks with the chunk index XOR-swizzled by
+// (row & 7), so both the row-wise global->LDS writes and the column-wise
+// fragment reads (32 rows, same chunk) are bank-conflict free.  The next
+// K-tile is fetched into registers while the current one feeds the MFMAs.
+// Block ids are remapped so that the tiles of one XCD (workgroups are dealt
+// round-robin over the 8 XCDs) form a compact group of output tiles sharing
+// A rows and W rows in that XCD's L2.
+#include "tk_common.hpp"
+
+namespace tk {
+namespace {
+
+constexpr int kBK = 64;  // K per LDS stage: 8 x 16-byte chunks per row
+
+struct GemmArgs {
+  const f16* a;
+  const f16* w;
+  const float* bias;
+  const float* resid;
+  void* c;
+  const float* ln_w;
+  const float* ln_b;
+  float* sum_out;
+  int64_t lda, ldw, ldr, ldc;
+  int M, N, K;
+  float eps;
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+
+// Maps the hardware block id to an output tile (tm, tn).  Consecutive
+// hardware ids go to different XCDs; the remap gives each XCD a contiguous
+// run of logical ids, and logical ids walk GROUP_M tile-rows at a time.
+__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int kXcd = 8, kGroupM = 8;
+  const int nb = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  const int full = nb - nb % kXcd;
+  if (id < full) id = (id % kXcd) * (full / kXcd) + id / kXcd;
+  const int per_group = kGroupM * tiles_n;
+  const int first_m = (id / per_group) * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int in_group = id % per_group;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Main loop: accumulates the (BN x BM) transposed tile into acc.
+// Wave (wm, wn) owns rows n in [wn*WN, +WN) and m in [wm*WM, +WM) of the tile.
+template <int BM, int BN, int WAVES_M, int WAVES_N>
+struct Mainloop {
+  static constexpr int NT = 64 * WAVES_M * WAVES_N;
+  static constexpr int WM = BM / WAVES_M;
+  static constexpr int WN = BN / WAVES_N;
+  static constexpr int FM = WM / 32;
+  static constexpr int FN = WN / 32;
+  static constexpr int A_LOADS = BM * 8 / NT;
+  static constexpr int W_LOADS = BN * 8 / NT;
+  static constexpr int LDS_HALVES = 2 * (BM + BN) * kBK;
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile chunks must divide threads");
+
+  __device__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % WAVES_M;
+    const int wn = wave / WAVES_M;
+    f16* As = smem;                  // [2][BM][64]
+    f16* Ws = smem + 2 * BM * kBK;   // [2][BN][64]
+
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    f16x8 ra[A_LOADS], rw[W_LOADS];
+    const int nk = (p.K + kBK - 1) / kBK;
+
+    auto gload = [&](int kt) {
+      const int k0 = kt * kBK;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        const int row = idx >> 3, ch = idx & 7;
+        const int gm = m0 + row, gk = k0 + ch * 8;
+        if (gm < p.M && gk < p.K)
+          ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
+        else
+          ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < W_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        const int row = idx >> 3, ch = idx & 7;
+        const int gn = n0 + row, gk = k0 + ch * 8;
+        if (gn < p.N && gk < p.K)
+          rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
+        else
+          rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    };
+    auto sstore = [&](int stage) {
+      f16* a_s = As + stage * BM * kBK;
+      f16* w_s = Ws + stage * BN * kBK;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        *reinterpret_cast<f16x8*>(a_s + swz(idx >> 3, idx & 7)) = ra[i];
+      }
+#pragma unroll
+      for (int i = 0; i < W_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        *reinterpret_cast<f16x8*>(w_s + swz(idx >> 3, idx & 7)) = rw[i];
+      }
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    const int frow = lane & 31;  // fragment row within a 32-row block
+    const int fhalf = lane >> 5; // which 8-wide k half of a 16-wide k step
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) gload(kt + 1);
+      const f16* a_s = As + cur * BM * kBK;
+      const f16* w_s = Ws + cur * BN * kBK;
+#pragma unroll
+      for (int kk = 0; kk < kBK / 16; ++kk) {
+        const int ch = 2 * kk + fhalf;
+        f16x8 fa[FM], fw[FN];
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz(wm * WM + j * 32 + frow, ch));
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz(wn * WN + i * 32 + frow, ch));
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
+      }
+      if (kt + 1 < nk) sstore(cur ^ 1);
+      __syncthreads();
+    }
+  }
+};
+
+// Output coordinates of accumulator element (i, j, q) for this lane:
+//   m = m_wave + j*32 + (lane & 31)
+//   n = n_wave + i*32 + 8*q + 4*(lane >> 5) + e,  e = 0..3  (acc index 4q+e)
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs p) {
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N>;
+  __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_of_block(tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  f32x16 acc[ML::FN][ML::FM];
+  ML::run(p, m0, n0, smem, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m_w = m0 + (wave % WAVES_M) * ML::WM + (lane & 31);
+  const int n_w = n0 + (wave / WAVES_M) * ML::WN + 4 * (lane >> 5);
+
+#pragma unroll
+  for (int i = 0; i < ML::FN; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n_w + i * 32 + 8 * q;
+      if (n >= p.N) continue;
+      const bool full = n + 3 < p.N;
+      float bv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.f;
+#pragma unroll
+      for (int j = 0; j < ML::FM; ++j) {
+        const int m = m_w + j * 32;
+        if (m >= p.M) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e] + bv[e];
+        if constexpr (EPI == TK_EPI_BIAS_RESID) {
+          const float* rr = p.resid + (int64_t)m * p.ldr + n;
+          float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
+          if (full) {
+            const f32x4 r = *reinterpret_cast<const f32x4*>(rr);
+            *reinterpret_cast<f32x4*>(cr) = f32x4{r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
+          } else {
+            for (int e = 0; e < 4 && n + e < p.N; ++e) cr[e] = rr[e] + v[e];
+          }
+        } else {
+          if constexpr (EPI == TK_EPI_BIAS_GELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+          }
+          f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
+          if (full) {
+            *reinterpret_cast<f16x4*>(cr) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          } else {
+            for (int e = 0; e < 4 && n + e < p.N; ++e) cr[e] = (f16)v[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Full-row variant: BN == N, so each block owns complete output rows and
+// finishes the residual add + LayerNorm + cast before anything leaves the
+// chip.  Row statistics: per-lane partial sums over its n values, the
+// lane-pair exchange (lanes l and l^32 hold the two n halves of each 8-wide
+// group), then across the WAVES_N waves through LDS.  Two passes (mean, then
+// mean of squared deviations) on register-resident values.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool H_HALF>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_ln_kernel(GemmArgs p) {
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N>;
+  __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
+  __shared__ float red[WAVES_N][BM];
+  const int tiles_m = (p.M + BM - 1) / BM;
+  int tm, tn;
+  tile_of_block(tiles_m, 1, tm, tn);
+  const int m0 = tm * BM;
+
+  f32x16 acc[ML::FN][ML::FM];
+  ML::run(p, m0, 0, smem, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int ml = wm * ML::WM + (lane & 31);  // tile-local row of fragment j=0
+  const int n_w = wn * ML::WN + 4 * (lane >> 5);
+
+  // s = resid + acc + bias, kept in acc.
+#pragma unroll
+  for (int i = 0; i < ML::FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n_w + i * 32 + 8 * q;
+      const f32x4 bv = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + n) : f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < ML::FM; ++j) {
+        const int m = m0 + ml + j * 32;
+        f32x4 r = {0, 0, 0, 0};
+        if (m < p.M) r = *reinterpret_cast<const f32x4*>(p.resid + (int64_t)m * p.ldr + n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += bv[e] + r[e];
+      }
+    }
+
+  // Row statistics, one row per (j, lane & 31).
+  float mean[ML::FM], rstd[ML::FM];
+#pragma unroll
+  for (int j = 0; j < ML::FM; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < ML::FN; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t += acc[i][j][r];
+    t += __shfl_xor(t, 32);
+    if (lane < 32) red[wn][ml + j * 32] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < ML::FM; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES_N; ++w) t += red[w][ml + j * 32];
+    mean[j] = t / (float)p.N;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < ML::FM; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < ML::FN; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float d = acc[i][j][r] - mean[j];
+        t += d * d;
+      }
+    t += __shfl_xor(t, 32);
+    if (lane < 32) red[wn][ml + j * 32] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < ML::FM; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES_N; ++w) t += red[w][ml + j * 32];
+    rstd[j] = 1.0f / sqrtf(t / (float)p.N + p.eps);
+  }
+
+#pragma unroll
+  for (int i = 0; i < ML::FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n_w + i * 32 + 8 * q;
+      const f32x4 gw = *reinterpret_cast<const f32x4*>(p.ln_w + n);
+      const f32x4 gb = *reinterpret_cast<const f32x4*>(p.ln_b + n);
+#pragma unroll
+      for (int j = 0; j < ML::FM; ++j) {
+        const int m = m0 + ml + j * 32;
+        if (m >= p.M) continue;
+        float s[4], h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] = acc[i][j][4 * q + e];
+          h[e] = (s[e] - mean[j]) * rstd[j] * gw[e] + gb[e];
+        }
+        if (p.sum_out)
+          *reinterpret_cast<f32x4*>(p.sum_out + (int64_t)m * p.N + n) = f32x4{s[0], s[1], s[2], s[3]};
+        if constexpr (H_HALF) {
+          *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(p.c) + (int64_t)m * p.N + n) =
+              f16x4{(f16)h[0], (f16)h[1], (f16)h[2], (f16)h[3]};
+        } else {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.c) + (int64_t)m * p.N + n) =
+              f32x4{h[0], h[1], h[2], h[3]};
+        }
+      }
+    }
+}
+
+template <int BM, int BN, int WM_, int WN_, int EPI>
+int launch_gemm(const GemmArgs& p, hipStream_t st) {
+  const int64_t tiles = (int64_t)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM_, WN_, EPI>), dim3((unsigned)tiles),
+                     dim3(64 * WM_ * WN_), 0, st, p);
+  return check_launch("tk_gemm");
+}
+
+template <int EPI>
+int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
+  const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  // Large tiles once they alone fill the 256 CUs; 128x128 while that tiling
+  // does; 64x64 for the small, launch-bound shapes.
+  if (t256 >= 240) return launch_gemm<256, 256, 2, 4, EPI>(p, st);
+  if (t128 >= 200) return launch_gemm<128, 128, 2, 2, EPI>(p, st);
+  return launch_gemm<64, 64, 1, 1, EPI>(p, st);
+}
+
+template <int BM, int BN, int WM_, int WN_>
+int launch_gemm_ln(const GemmArgs& p, bool h_half, hipStream_t st) {
+  const unsigned tiles = (unsigned)((p.M + BM - 1) / BM);
+  if (h_half)
+    hipLaunchKernelGGL((gemm_ln_kernel<BM, BN, WM_, WN_, true>), dim3(tiles), dim3(64 * WM_ * WN_),
+                       0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_ln_kernel<BM, BN, WM_, WN_, false>), dim3(tiles), dim3(64 * WM_ * WN_),
+                       0, st, p);
+  return check_launch("tk_gemm_bias_add_ln");
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace
+}  // namespace tk
+
+using namespace tk;
+
+extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t ldw,
+                       const float* bias, const float* resid, int64_t ldr, void* c, int64_t ldc,
+                       int64_t m, int64_t n, int64_t k, int epilogue, void* stream) {
+  TK_REQUIRE(a && w && c, TK_ERR_ARG, "tk_gemm: null pointer");
+  TK_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
+             TK_ERR_ARG, "tk_gemm: bad sizes m=%lld n=%lld k=%lld", (long long)m, (long long)n,
+             (long long)k);
+  TK_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k, TK_ERR_ARG,
+             "tk_gemm: k=%lld lda=%lld ldw=%lld must be multiples of 8 with ld >= k", (long long)k,
+             (long long)lda, (long long)ldw);
+  TK_REQUIRE(aligned16(a) && aligned16(w), TK_ERR_ARG, "tk_gemm: A and W must be 16-byte aligned");
+  TK_REQUIRE(epilogue == TK_EPI_BIAS || epilogue == TK_EPI_BIAS_GELU || epilogue == TK_EPI_BIAS_RESID,
+             TK_ERR_ARG, "tk_gemm: bad epilogue %d", epilogue);
+  TK_REQUIRE(ldc >= n, TK_ERR_ARG, "tk_gemm: ldc=%lld < n=%lld", (long long)ldc, (long long)n);
+  if (epilogue == TK_EPI_BIAS_RESID) {
+    TK_REQUIRE(resid != nullptr && ldr >= n, TK_ERR_ARG, "tk_gemm: residual epilogue needs resid, ldr >= n");
+    TK_REQUIRE(aligned16(resid) && aligned16(c) && ldr % 4 == 0 && ldc % 4 == 0, TK_ERR_ARG,
+               "tk_gemm: residual epilogue needs 16-byte aligned fp32 rows");
+  } else {
+    TK_REQUIRE(((uintptr_t)c & 7) == 0 && ldc % 4 == 0, TK_ERR_ARG,
+               "tk_gemm: fp16 output needs 8-byte aligned rows (ldc %% 4 == 0)");
+  }
+  if (m == 0 || n == 0) return TK_OK;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const f16*>(a);
+  p.w = reinterpret_cast<const f16*>(w);
+  p.bias = bias;
+  p.resid = resid;
+  p.c = c;
+  p.lda = lda; p.ldw = ldw; p.ldr = ldr; p.ldc = ldc;
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  hipStream_t st = as_stream(stream);
+  switch (epilogue) {
+    case TK_EPI_BIAS: return gemm_dispatch<TK_EPI_BIAS>(p, st);
+    case TK_EPI_BIAS_GELU: return gemm_dispatch<TK_EPI_BIAS_GELU>(p, st);
+    default: return gemm_dispatch<TK_EPI_BIAS_RESID>(p, st);
+  }
+}
+
+extern "C" int tk_gemm_ln_supported(int64_t n) { return n == 128 || n == 256 || n == 512; }
+
+extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half* w, int64_t ldw,
+                                   const float* bias, const float* resid, const float* ln_w,
+                                   const float* ln_b, float* sum_out, void* h_out, int h_dtype,
+                                   int64_t m, int64_t n, int64_t k, float eps, void* stream) {
+  TK_REQUIRE(a && w && resid && ln_w && ln_b && h_out, TK_ERR_ARG, "tk_gemm_bias_add_ln: null pointer");
+  TK_REQUIRE(tk_gemm_ln_supported(n), TK_ERR_UNSUPPORTED,
+             "tk_gemm_bias_add_ln: row width n=%lld not in {128, 256, 512}", (long long)n);
+  TK_REQUIRE(m >= 0 && m < (1ll << 31) && k >= 0 && k < (1ll << 31), TK_ERR_ARG,
+             "tk_gemm_bias_add_ln: bad sizes");
+  TK_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k, TK_ERR_ARG,
+             "tk_gemm_bias_add_ln: k, lda, ldw must be multiples of 8 with ld >= k");
+  TK_REQUIRE(h_dtype == TK_F16 || h_dtype == TK_F32, TK_ERR_ARG, "tk_gemm_bias_add_ln: bad h_dtype");
+  TK_REQUIRE(aligned16(a) && aligned16(w) && aligned16(resid) && aligned16(ln_w) && aligned16(ln_b) &&
+                 aligned16(h_out) && (sum_out == nullptr || aligned16(sum_out)) &&
+                 (bias == nullptr || aligned16(bias)),
+             TK_ERR_ARG, "tk_gemm_bias_add_ln: buffers must be 16-byte aligned");
+  if (m == 0) return TK_OK;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const f16*>(a);
+  p.w = reinterpret_cast<const f16*>(w);
+  p.bias = bias;
+  p.resid = resid;
+  p.c = h_out;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.sum_out = sum_out;
+  p.lda = lda; p.ldw = ldw; p.ldr = n; p.ldc = n;
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.eps = eps;
+  hipStream_t st = as_stream(stream);
+  const bool hh = h_dtype == TK_F16;
+  if (n == 512) return launch_gemm_ln<64, 512, 1, 8>(p, hh, st);
+  if (n == 256) return launch_gemm_ln<64, 256, 1, 4>(p, hh, st);
+  return launch_gemm_ln<64, 128, 1, 2>(p, hh, st);
+}

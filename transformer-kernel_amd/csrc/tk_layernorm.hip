@@ -1,0 +1,226 @@
+// Standalone LayerNorm(+residual add)+cast kernels, HBM-bound.
+//
+// One row is owned by a group of LPR lanes (16, 32 or 64) of a wave; the
+// whole row lives in registers, so the statistics are the exact two-pass
+// ones (mean, then mean of squared deviations: population variance) with one
+// HBM read and one write per element.  Row reductions are butterfly shuffles
+// inside the lane group -- no LDS, no __syncthreads.
+//
+// Numerics follow src/fused_kernels.py:80-161: fp32 add, fp32 statistics,
+// y = (s - mean) * rstd * w + b, cast last.
+#include "tk_common.hpp"
+
+namespace tk {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename T>
+struct Vec;
+template <>
+struct Vec<float> {
+  static __device__ __forceinline__ void load4(const float* p, float* v) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(p);
+    v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+  }
+  static __device__ __forceinline__ void store4(float* p, const float* v) {
+    f32x4 t = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p) = t;
+  }
+  static __device__ __forceinline__ float load1(const float* p) { return *p; }
+  static __device__ __forceinline__ void store1(float* p, float v) { *p = v; }
+};
+template <>
+struct Vec<f16> {
+  static __device__ __forceinline__ void load4(const f16* p, float* v) {
+    f16x4 t = *reinterpret_cast<const f16x4*>(p);
+    v[0] = (float)t[0]; v[1] = (float)t[1]; v[2] = (float)t[2]; v[3] = (float)t[3];
+  }
+  static __device__ __forceinline__ void store4(f16* p, const float* v) {
+    f16x4 t = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *reinterpret_cast<f16x4*>(p) = t;
+  }
+  static __device__ __forceinline__ float load1(const f16* p) { return (float)*p; }
+  static __device__ __forceinline__ void store1(f16* p, float v) { *p = (f16)v; }
+};
+
+// HAS_Y: s = x + y (residual add) else s = x.
+template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT>
+__global__ __launch_bounds__(kBlock) void ln_rows_kernel(
+    const float* x, const YT* __restrict__ y, const float* __restrict__ w,
+    const float* __restrict__ b, float* sum_out, OT* __restrict__ out, int64_t rows,
+    int cols, float eps) {
+  constexpr int kRowsPerBlock = kBlock / LPR;
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
+  if (row >= rows) return;
+
+  const float* xr = x + row * cols;
+  float s[NV * VW];
+
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c0 = (v * LPR + lane) * VW;
+    if constexpr (VW == 4) {
+      if (c0 < cols) {
+        Vec<float>::load4(xr + c0, &s[v * 4]);
+        if constexpr (HAS_Y) {
+          float t[4];
+          Vec<YT>::load4(y + row * cols + c0, t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[v * 4 + e] += t[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[v * 4 + e] = 0.f;
+      }
+    } else {
+      if (c0 < cols) {
+        s[v] = xr[c0];
+        if constexpr (HAS_Y) s[v] += Vec<YT>::load1(y + row * cols + c0);
+      } else {
+        s[v] = 0.f;
+      }
+    }
+  }
+
+  if (HAS_Y && sum_out != nullptr) {
+    float* sr = sum_out + row * cols;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int c0 = (v * LPR + lane) * VW;
+      if (c0 < cols) {
+        if constexpr (VW == 4) Vec<float>::store4(sr + c0, &s[v * 4]);
+        else sr[c0] = s[v];
+      }
+    }
+  }
+
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV * VW; ++i) acc += s[i];
+  const float mean = group_sum<LPR>(acc) / (float)cols;
+
+  acc = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c0 = (v * LPR + lane) * VW;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float d = (c0 + e < cols) ? s[v * VW + e] - mean : 0.f;
+      s[v * VW + e] = d;
+      acc += d * d;
+    }
+  }
+  const float var = group_sum<LPR>(acc) / (float)cols;
+  const float rstd = 1.0f / sqrtf(var + eps);
+
+  OT* orow = out + row * cols;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c0 = (v * LPR + lane) * VW;
+    if (c0 < cols) {
+      if constexpr (VW == 4) {
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(w + c0);
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(b + c0);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = s[v * 4 + e] * rstd * wv[e] + bv[e];
+        Vec<OT>::store4(orow + c0, o);
+      } else {
+        Vec<OT>::store1(orow + c0, s[v] * rstd * w[c0] + b[c0]);
+      }
+    }
+  }
+}
+
+template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT>
+int launch_rows(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
+                OT* out, int64_t rows, int cols, float eps, hipStream_t st) {
+  constexpr int kRowsPerBlock = kBlock / LPR;
+  const int64_t grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, YT, OT>), dim3((unsigned)grid),
+                     dim3(kBlock), 0, st, x, y, w, b, sum_out, out, rows, cols, eps);
+  return check_launch("layernorm");
+}
+
+// Picks lanes-per-row and register-vector count for `cols`.
+template <bool HAS_Y, typename YT, typename OT>
+int dispatch(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
+             OT* out, int64_t rows, int cols, float eps, hipStream_t st) {
+#define TK_LN(LPR, NV, VW) \
+  return launch_rows<LPR, NV, VW, HAS_Y, YT, OT>(x, y, w, b, sum_out, out, rows, cols, eps, st)
+  // 16-byte vector path needs cols % 4 == 0 and 16-byte aligned fp32 rows
+  // (8-byte for fp16 rows); anything else takes the scalar path.
+  auto al = [](const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; };
+  const bool vec_ok = cols % 4 == 0 && al(x, 16) && al(w, 16) && al(b, 16) && al(sum_out, 16) &&
+                      al(y, sizeof(YT) * 4) && al(out, sizeof(OT) * 4);
+  if (vec_ok) {
+    if (cols <= 64) TK_LN(16, 1, 4);
+    if (cols <= 128) TK_LN(32, 1, 4);
+    const int nv = (cols + 255) / 256;
+    if (nv <= 1) TK_LN(64, 1, 4);
+    if (nv <= 2) TK_LN(64, 2, 4);
+    if (nv <= 3) TK_LN(64, 3, 4);
+    if (nv <= 4) TK_LN(64, 4, 4);
+    if (nv <= 6) TK_LN(64, 6, 4);
+    if (nv <= 8) TK_LN(64, 8, 4);
+    if (nv <= 16) TK_LN(64, 16, 4);
+    TK_LN(64, 32, 4);
+  }
+  const int nv = (cols + 63) / 64;
+  if (nv <= 1) TK_LN(64, 1, 1);
+  if (nv <= 2) TK_LN(64, 2, 1);
+  if (nv <= 4) TK_LN(64, 4, 1);
+  if (nv <= 8) TK_LN(64, 8, 1);
+  if (nv <= 16) TK_LN(64, 16, 1);
+  if (nv <= 32) TK_LN(64, 32, 1);
+  if (nv <= 64) TK_LN(64, 64, 1);
+  TK_LN(64, 128, 1);
+#undef TK_LN
+}
+
+constexpr int64_t kMaxCols = 8192;
+
+}  // namespace
+}  // namespace tk
+
+using namespace tk;
+
+extern "C" int tk_ln_cast(const float* x, const float* w, const float* b, void* out,
+                          int out_dtype, int64_t rows, int64_t cols, float eps, void* stream) {
+  TK_REQUIRE(x && w && b && out, TK_ERR_ARG, "tk_ln_cast: null pointer");
+  TK_REQUIRE(rows >= 0 && cols >= 1 && cols <= kMaxCols, TK_ERR_ARG,
+             "tk_ln_cast: rows=%lld cols=%lld outside [0, inf) x [1, %lld]", (long long)rows,
+             (long long)cols, (long long)kMaxCols);
+  TK_REQUIRE(out_dtype == TK_F16 || out_dtype == TK_F32, TK_ERR_ARG,
+             "tk_ln_cast: bad out_dtype %d", out_dtype);
+  if (rows == 0) return TK_OK;
+  hipStream_t st = as_stream(stream);
+  const int c = (int)cols;
+  if (out_dtype == TK_F16)
+    return dispatch<false, float, f16>(x, nullptr, w, b, nullptr, (f16*)out, rows, c, eps, st);
+  return dispatch<false, float, float>(x, nullptr, w, b, nullptr, (float*)out, rows, c, eps, st);
+}
+
+extern "C" int tk_add_ln_cast(const float* x, const void* y, int y_dtype, const float* w,
+                              const float* b, float* sum_out, void* h_out, int h_dtype,
+                              int64_t rows, int64_t cols, float eps, void* stream) {
+  TK_REQUIRE(x && y && w && b && h_out, TK_ERR_ARG, "tk_add_ln_cast: null pointer");
+  TK_REQUIRE(rows >= 0 && cols >= 1 && cols <= kMaxCols, TK_ERR_ARG,
+             "tk_add_ln_cast: rows=%lld cols=%lld outside [0, inf) x [1, %lld]",
+             (long long)rows, (long long)cols, (long long)kMaxCols);
+  TK_REQUIRE((y_dtype == TK_F16 || y_dtype == TK_F32) && (h_dtype == TK_F16 || h_dtype == TK_F32),
+             TK_ERR_ARG, "tk_add_ln_cast: bad dtype (y=%d, h=%d)", y_dtype, h_dtype);
+  if (rows == 0) return TK_OK;
+  hipStream_t st = as_stream(stream);
+  const int c = (int)cols;
+  if (y_dtype == TK_F16) {
+    if (h_dtype == TK_F16)
+      return dispatch<true, f16, f16>(x, (const f16*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, st);
+    return dispatch<true, f16, float>(x, (const f16*)y, w, b, sum_out, (float*)h_out, rows, c, eps, st);
+  }
+  if (h_dtype == TK_F16)
+    return dispatch<true, float, f16>(x, (const float*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, st);
+  return dispatch<true, float, float>(x, (const float*)y, w, b, sum_out, (float*)h_out, rows, c, eps, st);
+}

@@ -1,0 +1,238 @@
+"""``OptimizedTransformer``: the reference's drop-in model on MI355X kernels.
+
+Interface (src/optimized.py:85-157,200-232,393-408):
+  * ``OptimizedTransformer(config, settings=None)`` subclasses
+    ``BaselineTransformer`` so ``state_dict`` keys match the baseline's and the
+    harness's strict weight copy works; no parameters or persistent buffers
+    are added (packed weights are plain attributes, dropped in ``_apply``).
+  * ``forward(x, valid_token_mask=None) -> Tensor`` returns ``[B, S, D]`` in
+    ``x.dtype``.
+  * ``OptimizerSettings`` / ``configure(**kw)`` / ``active_settings()``: the
+    harness constructs the model with no extra arguments, so settings are a
+    module-level default.
+
+Per layer the forward launches five kernels (src/optimized.py:488-554 is the
+reference schedule it replaces):
+
+  1. QKV GEMM       h[T,D] . Wqkv[3D,D]^T + b          -> qkv fp16 [T, 3D]
+  2. attention      flash forward over strided q/k/v    -> ctx fp16 [B, S, H*hd]
+  3. out-proj GEMM  + residual + LayerNorm2 + cast      -> resid fp32, h fp16
+  4. FFN-up GEMM    + bias + exact GELU                 -> u fp16 [T, F]
+  5. FFN-down GEMM  + residual + LayerNorm(next) + cast -> resid fp32, h fp16
+                    (the last layer's applies final_norm and writes fp32 out)
+
+plus one LayerNorm before the first layer.  Steps 3 and 5 run as one kernel
+when a whole row fits a GEMM tile (d_model in {128, 256, 512}); otherwise as
+a residual-epilogue GEMM followed by the standalone LayerNorm kernel.  The
+residual stream and all statistics stay fp32; only GEMM/attention operands
+are fp16 (docs/pass1-decisions.md:41-65 of the reference).
+"""
+
+from __future__ import annotations
+
+import weakref
+from dataclasses import dataclass, replace
+from typing import List, Optional
+
+import torch
+
+from . import ops
+from .modules import BaselineTransformer
+
+__all__ = ["OptimizerSettings", "OptimizedTransformer", "configure", "active_settings"]
+
+
+@dataclass(frozen=True)
+class OptimizerSettings:
+    """Knobs of the MI355X path (counterpart of src/optimized.py:85-139).
+
+    fused_norm        -- fuse residual + LayerNorm + cast into the out-proj /
+                         FFN-down GEMM epilogue where a row fits one tile; off
+                         uses the residual-epilogue GEMM + standalone
+                         LayerNorm kernel for every width (both are HIP).
+    assume_dense_mask -- skip the one device->host sync per new mask object
+                         that checks the padding mask is all-True.
+    """
+
+    fused_norm: bool = True
+    assume_dense_mask: bool = False
+
+
+_ACTIVE = OptimizerSettings()
+
+
+def configure(**kwargs) -> OptimizerSettings:
+    """Set the settings used by ``OptimizedTransformer(config)`` (src/optimized.py:145-153)."""
+    global _ACTIVE
+    _ACTIVE = replace(_ACTIVE, **kwargs)
+    return _ACTIVE
+
+
+def active_settings() -> OptimizerSettings:
+    return _ACTIVE
+
+
+@dataclass
+class _LayerWeights:
+    """One block's weights packed for the kernels.
+
+    GEMM weights fp16 (``[out, in]``, K-contiguous); biases and LayerNorm
+    parameters stay fp32 (biases are added to the fp32 accumulator).
+    """
+
+    n1_w: torch.Tensor
+    n1_b: torch.Tensor
+    n1_eps: float
+    w_qkv: torch.Tensor  # [3D, D] = cat(Wq, Wk, Wv)
+    b_qkv: torch.Tensor  # [3D]
+    w_o: torch.Tensor
+    b_o: torch.Tensor
+    n2_w: torch.Tensor
+    n2_b: torch.Tensor
+    n2_eps: float
+    w_1: torch.Tensor  # [F, D]
+    b_1: torch.Tensor
+    w_2: torch.Tensor  # [D, F]
+    b_2: torch.Tensor
+
+
+class OptimizedTransformer(BaselineTransformer):
+    """Drop-in replacement for the harness's ``UserOptimizedTransformer``."""
+
+    def __init__(self, config, settings: Optional[OptimizerSettings] = None) -> None:
+        super().__init__(config)
+        self.settings = settings if settings is not None else _ACTIVE
+        self.d_model = config.d_model
+        self.num_heads = config.num_heads
+        self.head_dim = config.d_model // config.num_heads
+        self.attn_scale = self.head_dim ** -0.5
+        self._weight_cache: Optional[List[_LayerWeights]] = None
+        self._weight_cache_key: Optional[tuple] = None
+        self._dense_mask_ref: Optional[weakref.ReferenceType] = None
+        self._dense_mask_value = False
+
+    # -- caches ------------------------------------------------------------- #
+
+    def _apply(self, *args, **kwargs):
+        result = super()._apply(*args, **kwargs)
+        self._weight_cache = None
+        self._weight_cache_key = None
+        return result
+
+    def _weights(self) -> List[_LayerWeights]:
+        """Packed weights, rebuilt when the device or any parameter changes.
+
+        The key includes every parameter's version counter, so an in-place
+        update (``load_state_dict`` after a forward) invalidates the cache.
+        """
+        params = list(self.parameters())
+        key = (params[0].device, sum(p._version for p in params), len(params))
+        if self._weight_cache is not None and self._weight_cache_key == key:
+            return self._weight_cache
+        f16 = lambda t: t.detach().to(torch.float16).contiguous()  # noqa: E731
+        f32 = lambda t: t.detach().to(torch.float32).contiguous()  # noqa: E731
+        built = []
+        with torch.no_grad():
+            for layer in self.layers:
+                at = layer.attention
+                built.append(
+                    _LayerWeights(
+                        n1_w=f32(layer.norm1.weight), n1_b=f32(layer.norm1.bias), n1_eps=layer.norm1.eps,
+                        w_qkv=f16(torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], 0)),
+                        b_qkv=f32(torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias], 0)),
+                        w_o=f16(at.out_proj.weight), b_o=f32(at.out_proj.bias),
+                        n2_w=f32(layer.norm2.weight), n2_b=f32(layer.norm2.bias), n2_eps=layer.norm2.eps,
+                        w_1=f16(layer.ffn_in.weight), b_1=f32(layer.ffn_in.bias),
+                        w_2=f16(layer.ffn_out.weight), b_2=f32(layer.ffn_out.bias),
+                    )
+                )
+        self._final = (f32(self.final_norm.weight), f32(self.final_norm.bias), self.final_norm.eps)
+        self._weight_cache = built
+        self._weight_cache_key = key
+        return built
+
+    def _mask_is_dense(self, valid_token_mask: Optional[torch.Tensor]) -> bool:
+        """True when no token is padded (src/optimized.py:362-389).
+
+        One device->host sync per distinct mask object, memoised by weakref
+        identity; the harness passes one mask object for all timed calls.
+        """
+        if valid_token_mask is None or self.settings.assume_dense_mask:
+            return True
+        if self._dense_mask_ref is None or self._dense_mask_ref() is not valid_token_mask:
+            self._dense_mask_value = bool(valid_token_mask.all())
+            self._dense_mask_ref = weakref.ref(valid_token_mask)
+        return self._dense_mask_value
+
+    # -- forward ------------------------------------------------------------ #
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError(
+                "OptimizedTransformer runs on the MI355X HIP kernels only; "
+                f"input is on {x.device}"
+            )
+        if x.dim() != 3 or x.shape[-1] != self.d_model:
+            raise ValueError(f"expected [B, S, {self.d_model}] input, got {tuple(x.shape)}")
+        if not self._mask_is_dense(valid_token_mask):
+            raise NotImplementedError(
+                "padded valid_token_mask is not supported by the MI355X kernels yet "
+                "(dense masks only)"
+            )
+        if not ops.attention_supported(self.head_dim, torch.float16, x.device):
+            raise NotImplementedError(f"head_dim {self.head_dim} is not supported by the attention kernel")
+        out = self._run_layers(x)
+        return out.to(x.dtype)
+
+    def _run_layers(self, x: torch.Tensor) -> torch.Tensor:
+        bsz, seq, d = x.shape
+        t = bsz * seq
+        nh, hd = self.num_heads, self.head_dim
+        weights = self._weights()
+        fn_w, fn_b, fn_eps = self._final
+        dev = x.device
+        xin = x.reshape(t, d)
+        if xin.dtype != torch.float32:
+            xin = xin.float()
+        xin = xin.contiguous()
+
+        resid = torch.empty((t, d), dtype=torch.float32, device=dev)
+        h = torch.empty((t, d), dtype=torch.float16, device=dev)
+        qkv = torch.empty((t, 3 * d), dtype=torch.float16, device=dev)
+        ctx = torch.empty((t, d), dtype=torch.float16, device=dev)
+        u = torch.empty((t, self.config.ffn_dim), dtype=torch.float16, device=dev)
+        out = torch.empty((t, d), dtype=torch.float32, device=dev)
+        fuse = self.settings.fused_norm and ops.gemm_ln_supported(d)
+
+        ops.ln_fwd(xin, weights[0].n1_w, weights[0].n1_b, weights[0].n1_eps, torch.float16, out=h,
+                   name="ln_in")
+        src = xin  # residual stream input of the next add (the caller's x is never written)
+        qkv5 = qkv.view(bsz, seq, 3, nh, hd)
+        q, k, v = qkv5.permute(2, 0, 3, 1, 4).unbind(0)  # [B, H, S, hd] strided views
+        ctx3 = ctx.view(bsz, seq, d)
+        last = len(weights) - 1
+        for i, lw in enumerate(weights):
+            ops.linear(h, lw.w_qkv, lw.b_qkv, out=qkv, name="qkv")
+            ops.flash_attention(q, k, v, self.attn_scale, self.config.causal, out=ctx3)
+            if fuse:
+                ops.linear_add_ln(ctx, lw.w_o, lw.b_o, src, lw.n2_w, lw.n2_b, lw.n2_eps,
+                                  sum_out=resid, h_out=h, name="out_proj_ln")
+            else:
+                ops.linear_residual(ctx, lw.w_o, lw.b_o, src, out=resid, name="out_proj_resid")
+                ops.ln_fwd(resid, lw.n2_w, lw.n2_b, lw.n2_eps, torch.float16, out=h, name="ln2")
+            src = resid
+            ops.linear(h, lw.w_1, lw.b_1, gelu=True, out=u, name="ffn_up_gelu")
+            if i < last:
+                nw, nb, neps = weights[i + 1].n1_w, weights[i + 1].n1_b, weights[i + 1].n1_eps
+                dst, keep_sum = h, True
+            else:
+                nw, nb, neps = fn_w, fn_b, fn_eps
+                dst, keep_sum = out, False  # final norm: the summed residual is dead
+            if fuse:
+                ops.linear_add_ln(u, lw.w_2, lw.b_2, resid, nw, nb, neps,
+                                  sum_out=resid if keep_sum else None, h_out=dst, name="ffn_down_ln")
+            else:
+                ops.linear_residual(u, lw.w_2, lw.b_2, resid, out=resid, name="ffn_down_resid")
+                ops.ln_fwd(resid, nw, nb, neps, dst.dtype, out=dst,
+                           name="ln_next" if keep_sum else "ln_final")
+        return out.view(bsz, seq, d)
