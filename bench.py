@@ -97,6 +97,8 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip the one-trial parity check")
+    ap.add_argument("--unfused-norm", action="store_true",
+                    help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -122,7 +124,8 @@ def main() -> int:
     torch.set_float32_matmul_precision("highest")
 
     base = ob.build_model(cfg, seed=1234).eval()
-    model = tkmi.OptimizedTransformer(tkmi.TransformerConfig(*cfg_t))
+    settings = tkmi.OptimizerSettings(fused_norm=not args.unfused_norm)
+    model = tkmi.OptimizedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
     ob.copy_model_weights(base, model, strict=True)
     model = model.to(dev).eval()
 
@@ -244,7 +247,7 @@ def main() -> int:
         "config": {
             "workload": f"{args.config}: B{b} S{s} D{d} H{h} F{f} L{nl} {'causal' if causal else 'non-causal'}",
             "batch": b, "seq_len": s, "d_model": d, "heads": h, "ffn_dim": f, "layers": nl,
-            "causal": causal, "parallelism": "single GPU",
+            "causal": causal, "parallelism": "single GPU", "fused_norm": not args.unfused_norm,
         },
         "tokens_per_s": round(t * 1000.0 / fwd_ms, 1),
         "wall_s_timed": round(wall, 4),

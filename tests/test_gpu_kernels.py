@@ -20,7 +20,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from conftest import or_rule_violations, seeded
+from conftest import fp16_excess, or_rule_violations, seeded
 from oracle import baseline as ob
 
 import tkmi
@@ -75,8 +75,7 @@ def test_layernorm_three_dim_and_noncontiguous():
     torch.testing.assert_close(y.cpu(), ob.layer_norm_ref(x + r.float(), w, b), atol=1e-5, rtol=1e-5)
     x3 = seeded(4, 16, 128, seed=25).transpose(0, 1)
     got = ops.ln_fwd(x3.to(DEV), w.to(DEV), b.to(DEV), 1e-5, torch.float16)
-    bad, err = or_rule_violations(got, ob.layer_norm_ref(x3, w, b, 1e-5, torch.float16), atol=1e-3, rtol=0)
-    assert bad == 0, err
+    assert fp16_excess(got, ob.layer_norm_ref(x3, w, b, 1e-5, torch.float16), atol=1e-3) <= 0
 
 
 @pytest.mark.parametrize("n_cols", [32, 128, 1024, 33, 100, 768, 2048])
@@ -86,14 +85,20 @@ def test_layernorm_script_matrix(n_cols):
     y = seeded(rows, n_cols, dtype=torch.float16, seed=n_cols + 1)
     w, b = seeded(n_cols, seed=n_cols + 2), seeded(n_cols, seed=n_cols + 3)
     xg, yg, wg, bg = x.to(DEV), y.to(DEV), w.to(DEV), b.to(DEV)
+    # fp32 out: |d| <= 1e-5; fp16 out: |d| <= max(1e-3, 1 fp16 ulp of the reference)
     for out_dtype, atol in ((torch.float32, 1e-5), (torch.float16, 1e-3)):
         got = ops.ln_fwd(xg, wg, bg, 1e-5, out_dtype)
         want = ob.layer_norm_ref(x, w, b, 1e-5, out_dtype)
-        assert (got.cpu().float() - want.float()).abs().max() <= atol
         s, h = ops.add_ln_fwd(xg, yg, wg, bg, 1e-5, out_dtype)
         sum_want = x + y.float()
+        h_want = ob.layer_norm_ref(sum_want, w, b, 1e-5, out_dtype)
         assert (s.cpu() - sum_want).abs().max() <= 1e-6
-        assert (h.cpu().float() - ob.layer_norm_ref(sum_want, w, b, 1e-5, out_dtype).float()).abs().max() <= atol
+        if out_dtype == torch.float32:
+            assert (got.cpu() - want).abs().max() <= atol
+            assert (h.cpu() - h_want).abs().max() <= atol
+        else:
+            assert fp16_excess(got, want, atol) <= 0
+            assert fp16_excess(h, h_want, atol) <= 0
 
 
 @pytest.mark.parametrize("cols", [512, 2048, 4096, 8192])

@@ -29,13 +29,17 @@ namespace {
 constexpr int kBN = 64;  // keys per tile
 
 // LDS byte offset of the 16-byte chunk `chunk` of row `row` in a tile whose
-// rows are RB bytes long, XOR-swizzled so that 8 consecutive rows read at
-// the same logical chunk hit 8 distinct bank groups.
+// rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane accesses
+// for 16 lanes per cycle from one 256-byte line of 64 banks, so the chunk
+// index is XOR-ed with the row's line number (modulo the chunks per row):
+// 16 consecutive rows read at one logical chunk then hit 16 distinct 16-byte
+// bank groups.
 template <int RB>
 __device__ __forceinline__ int swz_off(int row, int chunk) {
-  if constexpr (RB >= 128) return row * RB + ((chunk ^ (row & 7)) << 4);
-  else if constexpr (RB == 64) return row * RB + ((chunk ^ ((row >> 1) & 3)) << 4);
-  else return row * RB + ((chunk ^ ((row >> 2) & 1)) << 4);
+  if constexpr (RB >= 256) return row * RB + ((chunk ^ (row & 15)) << 4);
+  else if constexpr (RB == 128) return row * RB + ((chunk ^ ((row >> 1) & 7)) << 4);
+  else if constexpr (RB == 64) return row * RB + ((chunk ^ ((row >> 2) & 3)) << 4);
+  else return row * RB + ((chunk ^ ((row >> 3) & 1)) << 4);
 }
 
 // Position of key k (0..63 within the tile) in a V^T row: bits 2 and 3 swapped.

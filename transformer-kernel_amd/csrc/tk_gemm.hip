@@ -23,7 +23,8 @@
 namespace tk {
 namespace {
 
-constexpr int kBK = 64;  // K per LDS stage: 8 x 16-byte chunks per row
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct GemmArgs {
   const f16* a;
@@ -37,9 +38,41 @@ struct GemmArgs {
   int64_t lda, ldw, ldr, ldc;
   int M, N, K;
   float eps;
+  bool vec;  // output rows admit 4-wide vector stores
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+// LDS tile layout: rows of BK halves (BK = 64: 128 bytes = eight 16-byte
+// chunks; BK = 32: 64 bytes = four chunks).  The gfx950 LDS serves a
+// 16-byte-per-lane access for 16 lanes per cycle from 64 4-byte banks (one
+// 256-byte line = 2 or 4 tile rows).  The chunk index is XOR-ed with the
+// row's line number (mod chunks per row), so 16 consecutive rows read at one
+// logical chunk (a fragment load) and the row-wise copies both touch 16
+// distinct 16-byte bank groups.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  if constexpr (BK == 64) return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
+  else return row * 32 + ((chunk ^ ((row >> 2) & 3)) << 3);
+}
+
+// s_waitcnt with vmcnt <= N, other counters unconstrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the memory fence of __syncthreads() (which
+// waits for every outstanding vector-memory op, i.e. drains all in-flight
+// tile copies).  The empty asm statements keep the compiler from moving LDS
+// accesses across it; the direct-copy loop orders the copies itself with
+// wait_vmcnt, and every fragment read has completed before the MFMA that
+// consumes it was issued.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // Maps the hardware block id to an output tile (tm, tn).  Consecutive
 // hardware ids go to different XCDs; the remap gives each XCD a contiguous
@@ -60,18 +93,39 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& tm,
 
 // Main loop: accumulates the (BN x BM) transposed tile into acc.
 // Wave (wm, wn) owns rows n in [wn*WN, +WN) and m in [wm*WM, +WM) of the tile.
-template <int BM, int BN, int WAVES_M, int WAVES_N>
+//
+// DIRECT (K % BK == 0): K-tiles are copied global -> LDS with
+// global_load_lds_dwordx4, which writes a wave's 64 x 16 bytes to 1 KB of
+// LDS in lane order; lane l covers tile row r0 + l / (chunks per row) and
+// physical chunk l % (chunks per row), and fetches the logical chunk the
+// swizzle puts there.  Rows past M / N re-read the last valid row (their
+// outputs are never stored).  STAGES LDS buffers keep STAGES-1 tiles in
+// flight; after each tile the wave waits (vmcnt) only for the next tile's
+// copies, then one barrier.
+// Staged (K tail): 16-byte register prefetch of the next tile with zero fill
+// past M, N, K, two LDS buffers.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT>
 struct Mainloop {
-  static constexpr int NT = 64 * WAVES_M * WAVES_N;
+  static constexpr int NW = WAVES_M * WAVES_N;
+  static constexpr int NT = 64 * NW;
   static constexpr int WM = BM / WAVES_M;
   static constexpr int WN = BN / WAVES_N;
   static constexpr int FM = WM / 32;
   static constexpr int FN = WN / 32;
-  static constexpr int A_LOADS = BM * 8 / NT;
-  static constexpr int W_LOADS = BN * 8 / NT;
-  static constexpr int LDS_HALVES = 2 * (BM + BN) * kBK;
+  static constexpr int CPR = BK / 8;             // 16-byte chunks per tile row
+  static constexpr int RPC = 1024 / (BK * 2);    // tile rows per 1 KB wave copy
+  static constexpr int A_LOADS = BM * CPR / NT;  // staged: chunks per thread per tile
+  static constexpr int W_LOADS = BN * CPR / NT;
+  static constexpr int A_INSTS = BM / RPC / NW;  // direct: wave copies per tile
+  static constexpr int W_INSTS = BN / RPC / NW;
+  static constexpr int INSTS = A_INSTS + W_INSTS;
+  static constexpr int LDS_HALVES = STAGES * (BM + BN) * BK;
+  static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "tile chunks must divide threads");
+  static_assert(DIRECT || STAGES == 2, "the staged path double-buffers");
+  static_assert(!DIRECT || (BM % (RPC * NW) == 0 && BN % (RPC * NW) == 0), "copies must divide waves");
+  static_assert(DIRECT || ((BM * CPR) % NT == 0 && (BN * CPR) % NT == 0), "chunks must divide threads");
+  static_assert((STAGES - 2) * INSTS < 64, "vmcnt range");
 
   __device__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     const int tid = threadIdx.x;
@@ -79,8 +133,8 @@ struct Mainloop {
     const int wave = tid >> 6;
     const int wm = wave % WAVES_M;
     const int wn = wave / WAVES_M;
-    f16* As = smem;                  // [2][BM][64]
-    f16* Ws = smem + 2 * BM * kBK;   // [2][BN][64]
+    f16* As = smem;                      // [STAGES][BM][BK]
+    f16* Ws = smem + STAGES * BM * BK;   // [STAGES][BN][BK]
 
 #pragma unroll
     for (int i = 0; i < FN; ++i)
@@ -89,76 +143,129 @@ struct Mainloop {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    f16x8 ra[A_LOADS], rw[W_LOADS];
-    const int nk = (p.K + kBK - 1) / kBK;
+    const int nk = (p.K + BK - 1) / BK;
 
-    auto gload = [&](int kt) {
-      const int k0 = kt * kBK;
+    const f16* ga[DIRECT ? A_INSTS : 1];
+    const f16* gw[DIRECT ? W_INSTS : 1];
+    f16x8 ra[DIRECT ? 1 : A_LOADS], rw[DIRECT ? 1 : W_LOADS];
+
+    if constexpr (DIRECT) {
 #pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) {
-        const int idx = tid + i * NT;
-        const int row = idx >> 3, ch = idx & 7;
-        const int gm = m0 + row, gk = k0 + ch * 8;
-        if (gm < p.M && gk < p.K)
-          ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
-        else
-          ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < A_INSTS; ++i) {
+        const int r = (wave * A_INSTS + i) * RPC + lane / CPR;
+        const int c = swz<BK>(r, lane % CPR) - r * BK;  // physical -> logical is the same XOR
+        ga[i] = p.a + (int64_t)min(m0 + r, p.M - 1) * p.lda + c;
       }
 #pragma unroll
-      for (int i = 0; i < W_LOADS; ++i) {
-        const int idx = tid + i * NT;
-        const int row = idx >> 3, ch = idx & 7;
-        const int gn = n0 + row, gk = k0 + ch * 8;
-        if (gn < p.N && gk < p.K)
-          rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
-        else
-          rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < W_INSTS; ++i) {
+        const int r = (wave * W_INSTS + i) * RPC + lane / CPR;
+        const int c = swz<BK>(r, lane % CPR) - r * BK;
+        gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
+      }
+    }
+
+    auto issue = [&](int kt, int stage) {  // start tile kt's copy into `stage`
+      if constexpr (DIRECT) {
+        f16* a_s = As + stage * BM * BK;
+        f16* w_s = Ws + stage * BN * BK;
+#pragma unroll
+        for (int i = 0; i < A_INSTS; ++i)
+          __builtin_amdgcn_global_load_lds(ga[i] + kt * BK,
+                                           (lds_void*)(a_s + (wave * A_INSTS + i) * RPC * BK), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < W_INSTS; ++i)
+          __builtin_amdgcn_global_load_lds(gw[i] + kt * BK,
+                                           (lds_void*)(w_s + (wave * W_INSTS + i) * RPC * BK), 16, 0, 0);
+      } else {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) {
+          const int idx = tid + i * NT;
+          const int row = idx / CPR, ch = idx % CPR;
+          const int gm = m0 + row, gk = k0 + ch * 8;
+          if (gm < p.M && gk < p.K)
+            ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
+          else
+            ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < W_LOADS; ++i) {
+          const int idx = tid + i * NT;
+          const int row = idx / CPR, ch = idx % CPR;
+          const int gn = n0 + row, gk = k0 + ch * 8;
+          if (gn < p.N && gk < p.K)
+            rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
+          else
+            rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
       }
     };
-    auto sstore = [&](int stage) {
-      f16* a_s = As + stage * BM * kBK;
-      f16* w_s = Ws + stage * BN * kBK;
+    auto land = [&](int stage) {  // staged path: registers -> LDS
+      if constexpr (!DIRECT) {
+        f16* a_s = As + stage * BM * BK;
+        f16* w_s = Ws + stage * BN * BK;
 #pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) {
-        const int idx = tid + i * NT;
-        *reinterpret_cast<f16x8*>(a_s + swz(idx >> 3, idx & 7)) = ra[i];
-      }
+        for (int i = 0; i < A_LOADS; ++i) {
+          const int idx = tid + i * NT;
+          *reinterpret_cast<f16x8*>(a_s + swz<BK>(idx / CPR, idx % CPR)) = ra[i];
+        }
 #pragma unroll
-      for (int i = 0; i < W_LOADS; ++i) {
-        const int idx = tid + i * NT;
-        *reinterpret_cast<f16x8*>(w_s + swz(idx >> 3, idx & 7)) = rw[i];
+        for (int i = 0; i < W_LOADS; ++i) {
+          const int idx = tid + i * NT;
+          *reinterpret_cast<f16x8*>(w_s + swz<BK>(idx / CPR, idx % CPR)) = rw[i];
+        }
       }
     };
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
+    if constexpr (DIRECT) {
+#pragma unroll
+      for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s, s);
+      if (nk >= STAGES - 1) wait_vmcnt<(STAGES - 2) * INSTS>();
+      else wait_vmcnt<0>();
+      lds_barrier();
+    } else {
+      issue(0, 0);
+      land(0);
+      __syncthreads();
+    }
 
     const int frow = lane & 31;  // fragment row within a 32-row block
     const int fhalf = lane >> 5; // which 8-wide k half of a 16-wide k step
+    int cur = 0;
     for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) gload(kt + 1);
-      const f16* a_s = As + cur * BM * kBK;
-      const f16* w_s = Ws + cur * BN * kBK;
+      const bool more = kt + STAGES - 1 < nk;
+      if (more) {
+        const int nxt = cur == 0 ? STAGES - 1 : cur - 1;  // (kt + STAGES - 1) % STAGES
+        issue(kt + STAGES - 1, nxt);
+      }
+      const f16* a_s = As + cur * BM * BK;
+      const f16* w_s = Ws + cur * BN * BK;
 #pragma unroll
-      for (int kk = 0; kk < kBK / 16; ++kk) {
+      for (int kk = 0; kk < BK / 16; ++kk) {
         const int ch = 2 * kk + fhalf;
         f16x8 fa[FM], fw[FN];
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz(wm * WM + j * 32 + frow, ch));
+          fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
 #pragma unroll
         for (int i = 0; i < FN; ++i)
-          fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz(wn * WN + i * 32 + frow, ch));
+          fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
           for (int j = 0; j < FM; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
       }
-      if (kt + 1 < nk) sstore(cur ^ 1);
-      __syncthreads();
+      if constexpr (DIRECT) {
+        if (more) wait_vmcnt<(STAGES - 2) * INSTS>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+      } else {
+        if (more) land(cur ^ 1);
+        __syncthreads();
+      }
+      cur = cur + 1 == STAGES ? 0 : cur + 1;
     }
   }
 };
@@ -167,9 +274,22 @@ struct Mainloop {
 //   m = m_wave + j*32 + (lane & 31)
 //   n = n_wave + i*32 + 8*q + 4*(lane >> 5) + e,  e = 0..3  (acc index 4q+e)
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs p) {
-  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N>;
+// Tile configuration: block tile BM x BN, wave grid WAVES_M x WAVES_N, and
+// for the direct-copy path the K step and number of LDS stages.  The staged
+// (K-tail) path always runs K step 64 with two stages.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int BK = BK_, STAGES = STAGES_;
+  static constexpr int NT = 64 * WAVES_M_ * WAVES_N_;
+  template <bool DIRECT>
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT>;
+};
+
+template <class T, int EPI, bool DIRECT>
+__global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
+  constexpr int BM = T::BM, BN = T::BN, WAVES_M = T::WAVES_M;
+  using ML = typename T::template ML<DIRECT>;
   __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
@@ -191,7 +311,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs p
     for (int q = 0; q < 4; ++q) {
       const int n = n_w + i * 32 + 8 * q;
       if (n >= p.N) continue;
-      const bool full = n + 3 < p.N;
+      const bool full = p.vec && n + 3 < p.N;
       float bv[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.f;
@@ -234,9 +354,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs p
 // lane-pair exchange (lanes l and l^32 hold the two n halves of each 8-wide
 // group), then across the WAVES_N waves through LDS.  Two passes (mean, then
 // mean of squared deviations) on register-resident values.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool H_HALF>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_ln_kernel(GemmArgs p) {
-  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N>;
+template <class T, bool H_HALF, bool DIRECT>
+__global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
+  constexpr int BM = T::BM, WAVES_M = T::WAVES_M, WAVES_N = T::WAVES_N;
+  using ML = typename T::template ML<DIRECT>;
   __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
   __shared__ float red[WAVES_N][BM];
   const int tiles_m = (p.M + BM - 1) / BM;
@@ -343,34 +464,44 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_ln_kernel(GemmArg
     }
 }
 
-template <int BM, int BN, int WM_, int WN_, int EPI>
+template <class T, int EPI>
 int launch_gemm(const GemmArgs& p, hipStream_t st) {
-  const int64_t tiles = (int64_t)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM_, WN_, EPI>), dim3((unsigned)tiles),
-                     dim3(64 * WM_ * WN_), 0, st, p);
+  const int64_t tiles = (int64_t)((p.M + T::BM - 1) / T::BM) * ((p.N + T::BN - 1) / T::BN);
+  // The direct global->LDS copy needs whole K tiles.
+  if (p.K % T::BK == 0)
+    hipLaunchKernelGGL((gemm_kernel<T, EPI, true>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<T, EPI, false>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
   return check_launch("tk_gemm");
 }
+
+using TileBig = Tile<256, 256, 4, 2, 64, 2>;   // 8 waves of 64 x 128
+using TileMid = Tile<128, 128, 2, 2, 64, 2>;   // 4 waves of 64 x 64, 2 blocks per CU
+using TileSmall = Tile<64, 64, 1, 1, 64, 2>;   // 1 wave
 
 template <int EPI>
 int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  // Large tiles once they alone fill the 256 CUs; 128x128 while that tiling
-  // does; 64x64 for the small, launch-bound shapes.
-  if (t256 >= 240) return launch_gemm<256, 256, 2, 4, EPI>(p, st);
-  if (t128 >= 200) return launch_gemm<128, 128, 2, 2, EPI>(p, st);
-  return launch_gemm<64, 64, 1, 1, EPI>(p, st);
+  // Measured on MI355X: 256x256 tiles win only once K is long enough to
+  // amortise their prologue/epilogue (K >= 4096) and they fill the 256 CUs;
+  // 128x128 (2 blocks per CU) wins for shorter K; 64x64 for the small,
+  // launch-bound shapes.
+  if (p.K >= 4096 && t256 >= 240) return launch_gemm<TileBig, EPI>(p, st);
+  if (t128 >= 200) return launch_gemm<TileMid, EPI>(p, st);
+  return launch_gemm<TileSmall, EPI>(p, st);
 }
 
-template <int BM, int BN, int WM_, int WN_>
+template <class T>
 int launch_gemm_ln(const GemmArgs& p, bool h_half, hipStream_t st) {
-  const unsigned tiles = (unsigned)((p.M + BM - 1) / BM);
-  if (h_half)
-    hipLaunchKernelGGL((gemm_ln_kernel<BM, BN, WM_, WN_, true>), dim3(tiles), dim3(64 * WM_ * WN_),
-                       0, st, p);
-  else
-    hipLaunchKernelGGL((gemm_ln_kernel<BM, BN, WM_, WN_, false>), dim3(tiles), dim3(64 * WM_ * WN_),
-                       0, st, p);
+  const dim3 grid((unsigned)((p.M + T::BM - 1) / T::BM)), block(T::NT);
+  if (p.K % T::BK == 0) {
+    if (h_half) hipLaunchKernelGGL((gemm_ln_kernel<T, true, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((gemm_ln_kernel<T, false, true>), grid, block, 0, st, p);
+  } else {
+    if (h_half) hipLaunchKernelGGL((gemm_ln_kernel<T, true, false>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((gemm_ln_kernel<T, false, false>), grid, block, 0, st, p);
+  }
   return check_launch("tk_gemm_bias_add_ln");
 }
 
@@ -395,16 +526,16 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
   TK_REQUIRE(epilogue == TK_EPI_BIAS || epilogue == TK_EPI_BIAS_GELU || epilogue == TK_EPI_BIAS_RESID,
              TK_ERR_ARG, "tk_gemm: bad epilogue %d", epilogue);
   TK_REQUIRE(ldc >= n, TK_ERR_ARG, "tk_gemm: ldc=%lld < n=%lld", (long long)ldc, (long long)n);
-  if (epilogue == TK_EPI_BIAS_RESID) {
+  if (epilogue == TK_EPI_BIAS_RESID)
     TK_REQUIRE(resid != nullptr && ldr >= n, TK_ERR_ARG, "tk_gemm: residual epilogue needs resid, ldr >= n");
-    TK_REQUIRE(aligned16(resid) && aligned16(c) && ldr % 4 == 0 && ldc % 4 == 0, TK_ERR_ARG,
-               "tk_gemm: residual epilogue needs 16-byte aligned fp32 rows");
-  } else {
-    TK_REQUIRE(((uintptr_t)c & 7) == 0 && ldc % 4 == 0, TK_ERR_ARG,
-               "tk_gemm: fp16 output needs 8-byte aligned rows (ldc %% 4 == 0)");
-  }
   if (m == 0 || n == 0) return TK_OK;
   GemmArgs p{};
+  // 4-wide vector stores (and residual loads) when every output row start is
+  // aligned for them; element-wise otherwise.
+  if (epilogue == TK_EPI_BIAS_RESID)
+    p.vec = aligned16(resid) && aligned16(c) && ldr % 4 == 0 && ldc % 4 == 0;
+  else
+    p.vec = ((uintptr_t)c & 7) == 0 && ldc % 4 == 0;
   p.a = reinterpret_cast<const f16*>(a);
   p.w = reinterpret_cast<const f16*>(w);
   p.bias = bias;
@@ -453,7 +584,7 @@ extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half*
   p.eps = eps;
   hipStream_t st = as_stream(stream);
   const bool hh = h_dtype == TK_F16;
-  if (n == 512) return launch_gemm_ln<64, 512, 1, 8>(p, hh, st);
-  if (n == 256) return launch_gemm_ln<64, 256, 1, 4>(p, hh, st);
-  return launch_gemm_ln<64, 128, 1, 2>(p, hh, st);
+  if (n == 512) return launch_gemm_ln<Tile<64, 512, 1, 8, 64, 2>>(p, hh, st);
+  if (n == 256) return launch_gemm_ln<Tile<64, 256, 1, 4, 64, 2>>(p, hh, st);
+  return launch_gemm_ln<Tile<64, 128, 1, 2, 64, 2>>(p, hh, st);
 }
