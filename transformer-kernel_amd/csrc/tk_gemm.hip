@@ -104,7 +104,7 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& tm,
 // copies, then one barrier.
 // Staged (K tail): 16-byte register prefetch of the next tile with zero fill
 // past M, N, K, two LDS buffers.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT, int SCHED = 1>
 struct Mainloop {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = 64 * NW;
@@ -233,29 +233,69 @@ struct Mainloop {
     const int frow = lane & 31;  // fragment row within a 32-row block
     const int fhalf = lane >> 5; // which 8-wide k half of a 16-wide k step
     int cur = 0;
+    constexpr int KSTEPS = BK / 16;
     for (int kt = 0; kt < nk; ++kt) {
       const bool more = kt + STAGES - 1 < nk;
-      if (more) {
-        const int nxt = cur == 0 ? STAGES - 1 : cur - 1;  // (kt + STAGES - 1) % STAGES
-        issue(kt + STAGES - 1, nxt);
-      }
+      const int nxt = cur == 0 ? STAGES - 1 : cur - 1;  // (kt + STAGES - 1) % STAGES
+      if (!(DIRECT && SCHED == 1) && more) issue(kt + STAGES - 1, nxt);
       const f16* a_s = As + cur * BM * BK;
       const f16* w_s = Ws + cur * BN * BK;
-#pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        const int ch = 2 * kk + fhalf;
-        f16x8 fa[FM], fw[FN];
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
-#pragma unroll
-        for (int i = 0; i < FN; ++i)
-          fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
-#pragma unroll
-        for (int i = 0; i < FN; ++i)
+      if constexpr (DIRECT && SCHED == 1) {
+        // Fragments of step kk+1 are read while step kk's MFMAs run, and the
+        // next tile's copies are spread over the steps, so no step starts
+        // with a burst of memory instructions ahead of its MFMAs.
+        f16x8 fa[2][FM], fw[2][FN];
+        auto frags = [&](int buf, int kk) {
+          const int ch = 2 * kk + fhalf;
 #pragma unroll
           for (int j = 0; j < FM; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
+            fa[buf][j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            fw[buf][i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
+        };
+        frags(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          if (kk + 1 < KSTEPS) frags((kk + 1) & 1, kk + 1);
+          if (more) {
+            f16* a_n = As + nxt * BM * BK;
+            f16* w_n = Ws + nxt * BN * BK;
+            const int kn = (kt + STAGES - 1) * BK;
+#pragma unroll
+            for (int i = 0; i < A_INSTS; ++i)
+              if (i % KSTEPS == kk)
+                __builtin_amdgcn_global_load_lds(ga[i] + kn, (lds_void*)(a_n + (wave * A_INSTS + i) * RPC * BK),
+                                                 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < W_INSTS; ++i)
+              if ((A_INSTS + i) % KSTEPS == kk)
+                __builtin_amdgcn_global_load_lds(gw[i] + kn, (lds_void*)(w_n + (wave * W_INSTS + i) * RPC * BK),
+                                                 16, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[kk & 1][i], fa[kk & 1][j], acc[i][j], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          const int ch = 2 * kk + fhalf;
+          f16x8 fa[FM], fw[FN];
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
+        }
       }
       if constexpr (DIRECT) {
         if (more) wait_vmcnt<(STAGES - 2) * INSTS>();
@@ -277,13 +317,13 @@ struct Mainloop {
 // Tile configuration: block tile BM x BN, wave grid WAVES_M x WAVES_N, and
 // for the direct-copy path the K step and number of LDS stages.  The staged
 // (K-tail) path always runs K step 64 with two stages.
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_, int SCHED_ = 1>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int BK = BK_, STAGES = STAGES_;
   static constexpr int NT = 64 * WAVES_M_ * WAVES_N_;
   template <bool DIRECT>
-  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT>;
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT, SCHED_>;
 };
 
 template <class T, int EPI, bool DIRECT>

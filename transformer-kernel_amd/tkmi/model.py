@@ -22,8 +22,9 @@ reference schedule it replaces):
                     (the last layer's applies final_norm and writes fp32 out)
 
 plus one LayerNorm before the first layer.  Steps 3 and 5 run as one kernel
-when a whole row fits a GEMM tile (d_model in {128, 256, 512}); otherwise as
-a residual-epilogue GEMM followed by the standalone LayerNorm kernel.  The
+when a whole row fits a GEMM tile and is narrow enough for that to pay
+(d_model <= OptimizerSettings.fused_norm_max_d); otherwise as a
+residual-epilogue GEMM followed by the standalone LayerNorm kernel.  The
 residual stream and all statistics stay fp32; only GEMM/attention operands
 are fp16 (docs/pass1-decisions.md:41-65 of the reference).
 """
@@ -50,11 +51,17 @@ class OptimizerSettings:
                          FFN-down GEMM epilogue where a row fits one tile; off
                          uses the residual-epilogue GEMM + standalone
                          LayerNorm kernel for every width (both are HIP).
+    fused_norm_max_d  -- widest d_model that takes the fused epilogue.  Its
+                         full-row tiles (64 rows x d_model) re-read the whole
+                         weight panel per 64 rows; measured on MI355X at
+                         d_model 512 (C2) the split path is ~15% faster per
+                         forward, so the fused one is kept for narrow rows.
     assume_dense_mask -- skip the one device->host sync per new mask object
                          that checks the padding mask is all-True.
     """
 
     fused_norm: bool = True
+    fused_norm_max_d: int = 256
     assume_dense_mask: bool = False
 
 
@@ -202,7 +209,8 @@ class OptimizedTransformer(BaselineTransformer):
         ctx = torch.empty((t, d), dtype=torch.float16, device=dev)
         u = torch.empty((t, self.config.ffn_dim), dtype=torch.float16, device=dev)
         out = torch.empty((t, d), dtype=torch.float32, device=dev)
-        fuse = self.settings.fused_norm and ops.gemm_ln_supported(d)
+        fuse = (self.settings.fused_norm and d <= self.settings.fused_norm_max_d
+                and ops.gemm_ln_supported(d))
 
         ops.ln_fwd(xin, weights[0].n1_w, weights[0].n1_b, weights[0].n1_eps, torch.float16, out=h,
                    name="ln_in")
