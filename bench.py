@@ -97,6 +97,8 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip the one-trial parity check")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the whole forward replayed from a HIP graph (tkmi.graphs.GraphedTransformer)")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -128,6 +130,13 @@ def main() -> int:
     model = tkmi.OptimizedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
     ob.copy_model_weights(base, model, strict=True)
     model = model.to(dev).eval()
+    timed_model = model
+    if args.graph:
+        from tkmi.graphs import GraphedTransformer
+
+        timed_model = GraphedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
+        ob.copy_model_weights(base, timed_model, strict=True)
+        timed_model = timed_model.to(dev).eval()
 
     parity = None
     if not args.no_check and args.config in ("C1", "C2"):
@@ -146,15 +155,15 @@ def main() -> int:
     x, mask = x.to(dev), mask.to(dev)
 
     with torch.inference_mode():
-        for _ in range(args.warmup):
-            model(x, mask)
+        for _ in range(max(args.warmup, 10 if args.graph else 0)):
+            timed_model(x, mask)
         torch.cuda.synchronize()
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
         t0 = time.perf_counter()
         for i in range(args.steps):
             starts[i].record()
-            model(x, mask)
+            timed_model(x, mask)
             ends[i].record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -248,6 +257,7 @@ def main() -> int:
             "workload": f"{args.config}: B{b} S{s} D{d} H{h} F{f} L{nl} {'causal' if causal else 'non-causal'}",
             "batch": b, "seq_len": s, "d_model": d, "heads": h, "ffn_dim": f, "layers": nl,
             "causal": causal, "parallelism": "single GPU", "fused_norm": not args.unfused_norm,
+            "hip_graph": bool(args.graph),
         },
         "tokens_per_s": round(t * 1000.0 / fwd_ms, 1),
         "wall_s_timed": round(wall, 4),

@@ -280,3 +280,18 @@ def test_masked_softmax_key_lengths():
     want = torch.stack([ob.masked_softmax_ref(scores[g], True, valid[g // h]) for g in range(b * h)])
     want = torch.nan_to_num(want, nan=0.0)  # all-masked rows -> zeros
     assert (got.cpu().float() - want).abs().max() <= 1e-3
+
+
+def test_gelu_epilogue_dense_range():
+    """The GELU epilogue over a dense sweep of pre-activations: A = 0 so the
+    GEMM output is gelu(bias) exactly; compared with the exact-erf GELU cast
+    to fp16.  The kernel's erfc (Abramowitz & Stegun 7.1.26) carries
+    |GELU error| <= 0.75e-7*|x| <= 6e-7 on [-8, 8]; where |GELU| ~ 1e-3 one
+    fp16 ulp is ~1e-6, so the allowed difference is max(1 ulp, 2e-6)."""
+    n = 8192
+    bias = torch.linspace(-8.0, 8.0, n)
+    a = torch.zeros(64, 64, dtype=torch.float16, device=DEV)
+    w = torch.zeros(n, 64, dtype=torch.float16, device=DEV)
+    got = ops.linear(a, w, bias.to(DEV), gelu=True)
+    want = ob.gelu_ref(bias).half().float().expand(64, n)
+    assert fp16_excess(got, want, atol=2e-6) <= 0

@@ -161,3 +161,36 @@ def test_padded_mask_is_rejected_loudly():
     assert not bool(mask.all())
     with pytest.raises(NotImplementedError):
         opt(x.to(DEV), mask.to(DEV))
+
+
+def test_graphed_forward_replays_match_eager():
+    """Whole-forward HIP graph (src/cuda_graphs.py semantics): after the eager
+    warm-up calls the graph is captured; every replay -- with eager work and
+    synchronisations in between, and with fresh input tensors (copied into the
+    captured buffer) -- must equal the eager forward bit for bit."""
+    from tkmi.graphs import GraphedTransformer, WARMUP_BEFORE_CAPTURE
+
+    cfg = ob.TransformerConfig(4, 64, 128, 4, 256, 2, True)
+    base = ob.build_model(cfg, seed=11).eval()
+    eager = tkmi.OptimizedTransformer(tkmi.TransformerConfig(**cfg.__dict__))
+    graphed = GraphedTransformer(tkmi.TransformerConfig(**cfg.__dict__))
+    ob.copy_model_weights(base, eager)
+    ob.copy_model_weights(base, graphed)
+    eager, graphed = eager.to(DEV).eval(), graphed.to(DEV).eval()
+    inputs = [ob.generate_random_case(cfg, seed=100 + i)[0].to(DEV) for i in range(4)]
+    mask = torch.ones(cfg.batch_size, cfg.seq_len, dtype=torch.bool, device=DEV)
+    with torch.inference_mode():
+        for _ in range(WARMUP_BEFORE_CAPTURE):
+            graphed(inputs[0], mask)
+        for rep in range(6):
+            x = inputs[rep % len(inputs)]
+            got = graphed(x, mask).clone()
+            torch.cuda.synchronize()
+            want = eager(x, mask)  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"replay {rep} differs"
+        state = next(iter(graphed._graphs.values()))
+        assert state.graph is not None, "graph was not captured"
+        replayed = graphed(inputs[1], mask).cpu()
+        ref = base(inputs[1].cpu(), mask.cpu())
+    assert ob.compare_outputs(ref, replayed).passed

@@ -1,8 +1,10 @@
 // FlashAttention-2-style forward for gfx950 (fp16 MFMA, fp32 online softmax).
 //
-// Per workgroup: BM query rows of one (batch, head), one wave per 32 rows.
-// Key/value tiles of 64 keys are staged in LDS (two stages, next tile
-// prefetched into registers while the current one is consumed).
+// Per workgroup: BM = 32*NW query rows of one (batch, head), one wave per 32
+// rows.  Key/value tiles of 64 keys live in three LDS stages; K tiles are
+// copied global -> LDS directly (global_load_lds_dwordx4), V tiles go through
+// registers and are written transposed (V^T).  Tile t+2 is fetched while
+// tile t is consumed.
 //
 // Transposed formulation.  Each wave computes S^T = K . Q^T with
 // v_mfma_f32_32x32x16_f16 (A operand = K rows from LDS, B operand = the
@@ -17,16 +19,24 @@
 // LDS with key bits 2 and 3 swapped so that the matching A operand (8 keys
 // of one head-dim row d) is one contiguous 16-byte read.
 //
+// Software pipeline inside a wave: the S^T MFMAs of tile t+1 are issued
+// before the softmax of tile t, so the exp/max/sum VALU work of one tile runs
+// while the matrix core computes the next tile's scores.
+//
 // Numerics (src/kernels.py:112-134, src/torch_transformer_benchmark.py:97-111):
-// fp32 scores, scale applied in fp32 after Q.K^T (folded with log2(e) into
-// one multiply before exp2), -inf masking of future keys, fp32 running
-// max/sum, fp16 P for the PV product, fp32 accumulation, one final divide.
+// fp32 scores, the scale applied in fp32 after Q.K^T (folded with log2(e)
+// into one FMA before exp2: exp2(s*c - m*c) = exp(scale*(s - m))), -inf
+// masking of future keys, fp32 running max/sum, fp16 P for the PV product,
+// fp32 accumulation, one final divide.
 #include "tk_common.hpp"
 
 namespace tk {
 namespace {
 
-constexpr int kBN = 64;  // keys per tile
+constexpr int kBN = 64;     // keys per tile
+constexpr int kStages = 3;  // LDS stages (tile t read, t+1 read as "next K", t+2 landing)
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 // LDS byte offset of the 16-byte chunk `chunk` of row `row` in a tile whose
 // rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane accesses
@@ -42,6 +52,20 @@ __device__ __forceinline__ int swz_off(int row, int chunk) {
   else return row * RB + ((chunk ^ ((row >> 3) & 1)) << 4);
 }
 
+// Max / sum over the lane pair (l, l^32) that holds one query row.
+// v_permlane32_swap of a register with itself leaves, in every lane, its own
+// value in one half of the result and the partner's in the other, so a
+// symmetric op over both halves is the pair reduction -- two VALU ops, no
+// LDS round trip (a ds_bpermute would also wait on the in-flight K reads).
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Position of key k (0..63 within the tile) in a V^T row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
@@ -55,22 +79,29 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
 };
 
-template <int HD, int BM, bool CAUSAL>
-__global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
-  constexpr int NW = BM / 32;
+// The body is a __device__ function (the __global__ wrapper below only calls
+// it): device-only builtins used directly in a kernel template's lambdas
+// would make the host-side instantiation, and with it the launch stub, fail.
+template <int HD, int NW, bool CAUSAL>
+__device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
+  constexpr int BM = 32 * NW;
   constexpr int NT = NW * 64;
-  constexpr int KRB = HD * 2;            // K tile row bytes
-  constexpr int VRB = kBN * 2;           // V^T tile row bytes (128)
-  constexpr int K_CHUNKS = kBN * HD / 8; // 16-byte chunks per K tile
-  constexpr int K_LOADS = (K_CHUNKS + NT - 1) / NT;
-  constexpr int V_BLOCKS = kBN * HD / 16; // 4 keys x 4 dims micro-blocks
-  constexpr int V_LOADS = (V_BLOCKS + NT - 1) / NT;
+  constexpr int KRB = HD * 2;               // K tile row bytes
+  constexpr int VRB = kBN * 2;              // V^T tile row bytes (128)
   constexpr int KSTAGE = kBN * KRB;
   constexpr int VSTAGE = HD * VRB;
-  constexpr int DB = (HD + 31) / 32;     // 32-row blocks of the O^T accumulator
-  constexpr int KSTEPS = HD / 16;        // k16 steps of S^T = K.Q^T
+  constexpr int STAGE = KSTAGE + VSTAGE;
+  constexpr int K_COPIES = KSTAGE / 1024;   // 1 KB wave copies per K tile
+  constexpr int K_CPW = (K_COPIES + NW - 1) / NW;
+  constexpr int K_RPC = 1024 / KRB;         // K rows per copy
+  constexpr int K_CPR = KRB / 16;           // 16-byte chunks per K row
+  constexpr int V_BLOCKS = kBN * HD / 16;   // 4 keys x 4 dims micro-blocks
+  constexpr int V_LOADS = (V_BLOCKS + NT - 1) / NT;
+  constexpr int DB = (HD + 31) / 32;        // 32-row blocks of the O^T accumulator
+  constexpr int KSTEPS = HD / 16;           // k16 steps of S^T = K.Q^T
+  static_assert(KSTAGE % 1024 == 0, "K tile must be whole 1 KB copies");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * (KSTAGE + VSTAGE)];
+  __shared__ __attribute__((aligned(16))) char smem[kStages * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -91,6 +122,8 @@ __global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
 
   const int my_row = q0 + wave * 32 + (lane & 31);
   const int g = lane >> 5;
+  const int wave_row_min = q0 + wave * 32;
+  const int wave_row_max = wave_row_min + 31;
 
   // Q^T fragments (B operand): lane supplies Q[row][16*kk + 8*g .. +8].
   f16x8 qf[KSTEPS];
@@ -107,26 +140,38 @@ __global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
   for (int d = 0; d < DB; ++d)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_o[d][r] = 0.f;
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  float m_run = -INFINITY;  // running max of scale*log2e*s
+  float l_run = 0.f;        // lane-partial running sum (this lane's keys)
 
   const int kv_end = CAUSAL ? min(p.S, q0 + BM) : p.S;
   const int n_kt = (kv_end + kBN - 1) / kBN;
 
-  f16x8 rk[K_LOADS];
-  f16x4 rv[V_LOADS][4];
-
-  auto gload = [&](int kt) {
-    const int k0 = kt * kBN;
+  // ---- K tile: direct copies; per-lane source offsets fixed, tile stride added ----
+  int k_src_row[K_CPW], k_src_col[K_CPW];
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = tid + i * NT;
-      const int key = idx / (HD / 8), ch = idx % (HD / 8);
-      if (idx < K_CHUNKS && k0 + key < p.S)
-        rk[i] = *reinterpret_cast<const f16x8*>(kb + (int64_t)(k0 + key) * p.ks[2] + ch * 8);
-      else
-        rk[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < K_CPW; ++i) {
+    const int ci = wave + i * NW;
+    const int row = ci * K_RPC + lane / K_CPR;
+    k_src_row[i] = row;
+    k_src_col[i] = (swz_off<KRB>(row, lane % K_CPR) - row * KRB) >> 1;  // logical chunk, in halves
+  }
+  auto load_k = [&](int kt, int stage) {
+    char* ks_ = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < K_CPW; ++i) {
+      const int ci = wave + i * NW;
+      if (K_COPIES % NW == 0 || ci < K_COPIES) {
+        const int key = min(kt * kBN + k_src_row[i], p.S - 1);  // rows past S: finite, masked
+        __builtin_amdgcn_global_load_lds(kb + (int64_t)key * p.ks[2] + k_src_col[i],
+                                         (lds_void*)(ks_ + ci * 1024), 16, 0, 0);
+      }
     }
+  };
+
+  // ---- V tile: 4 keys x 4 dims per thread through registers, written as V^T ----
+  f16x4 rv[V_LOADS][4];
+  auto load_v = [&](int kt) {
+    const int k0 = kt * kBN;
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
       const int idx = tid + i * NT;
@@ -141,17 +186,8 @@ __global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
       }
     }
   };
-  auto sstore = [&](int stage) {
-    char* ks_ = smem + stage * (KSTAGE + VSTAGE);
-    char* vs_ = ks_ + KSTAGE;
-#pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < K_CHUNKS) {
-        const int key = idx / (HD / 8), ch = idx % (HD / 8);
-        *reinterpret_cast<f16x8*>(ks_ + swz_off<KRB>(key, ch)) = rk[i];
-      }
-    }
+  auto store_v = [&](int stage) {
+    char* vs_ = smem + stage * STAGE + KSTAGE;
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
       const int idx = tid + i * NT;
@@ -168,92 +204,133 @@ __global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
     }
   };
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  auto needs = [&](int kt) { return !CAUSAL || kt * kBN <= wave_row_max; };
 
-  const int wave_row_max = q0 + wave * 32 + 31;
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int cur = kt & 1;
-    const int k0 = kt * kBN;
-    if (kt + 1 < n_kt) gload(kt + 1);
-    const char* ks_ = smem + cur * (KSTAGE + VSTAGE);
-    const char* vs_ = ks_ + KSTAGE;
-
-    if (!CAUSAL || k0 <= wave_row_max) {
-      // ---- S^T = K . Q^T : two 32-key blocks ----
-      f32x16 sacc[2];
+  // ---- S^T = K . Q^T for one tile: two 32-key blocks ----
+  auto scores = [&](int stage, f32x16 (&sacc)[2]) {
+    const char* ks_ = smem + stage * STAGE;
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb2][r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[kb2][r] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const f16x8 kf =
-              *reinterpret_cast<const f16x8*>(ks_ + swz_off<KRB>(kb2 * 32 + (lane & 31), 2 * kk + g));
-          sacc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], sacc[kb2], 0, 0, 0);
-        }
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const f16x8 kf =
+            *reinterpret_cast<const f16x8*>(ks_ + swz_off<KRB>(kb2 * 32 + (lane & 31), 2 * kk + g));
+        sacc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], sacc[kb2], 0, 0, 0);
       }
-      // ---- mask, scale, running max ----
-      // accumulator entry r of block kb2 is key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4
-      const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > q0 + wave * 32);
-      float mx = -INFINITY;
+    }
+  };
+
+  // ---- softmax of one tile's scores + O^T += V^T . P^T ----
+  // accumulator entry r of block kb2 is key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4
+  auto softmax_pv = [&](int kt, int stage, f32x16 (&sacc)[2]) {
+    const int k0 = kt * kBN;
+    const char* vs_ = smem + stage * STAGE + KSTAGE;
+    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min);
+    float mx = -INFINITY;
+    if (need_mask) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float t = sacc[kb2][r] * p.scale_log2;
-          if (need_mask) {
-            const int key = k0 + kb2 * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= p.S || (CAUSAL && key > my_row)) t = -INFINITY;
-          }
-          sacc[kb2][r] = t;
-          mx = fmaxf(mx, t);
+          const int key = k0 + kb2 * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= p.S || (CAUSAL && key > my_row)) sacc[kb2][r] = -INFINITY;
+          mx = fmaxf(mx, sacc[kb2][r]);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      m_run = m_new;
-      float ls = 0.f;
-      f16x8 pf[4];
+    } else {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float pv = exp2f(sacc[kb2][hh * 8 + e] - m_use);
-            ls += pv;
-            pf[kb2 * 2 + hh][e] = (f16)pv;
-          }
-      l_run = l_run * alpha + ls;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
+    }
+    mx = pair_max(mx);
+    const float c = p.scale_log2;
+    const float m_tile = mx * c;  // c > 0: max(s)*c == max(s*c)
+    // Lazy rescale: the reference max m_run only moves when some row of the
+    // wave has grown by more than 2^8 over it, so exponentials stay <= 256
+    // (exact in fp16's range) and the O/l rescale is skipped on most tiles;
+    // O and l always share one reference, so the final O/l is unchanged.
+    if (__any(m_tile > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
-      // ---- O^T += V^T . P^T : four 16-key steps ----
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ls = 0.f;
+    f16x8 pf[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+    for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          const int drow = d * 32 + (lane & 31);
-          f16x8 vf;
-          if (HD % 32 == 0 || drow < HD)
-            vf = *reinterpret_cast<const f16x8*>(vs_ + swz_off<VRB>(drow, 2 * t + g));
-          else
-            vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-          acc_o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], acc_o[d], 0, 0, 0);
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][hh * 8 + e], c, -m_use));
+          ls += pv;
+          pf[kb2 * 2 + hh][e] = (f16)pv;
         }
+    l_run += ls;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int drow = d * 32 + (lane & 31);
+        f16x8 vf;
+        if (HD % 32 == 0 || drow < HD)
+          vf = *reinterpret_cast<const f16x8*>(vs_ + swz_off<VRB>(drow, 2 * t + g));
+        else
+          vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        acc_o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], acc_o[d], 0, 0, 0);
       }
     }
+  };
 
-    if (kt + 1 < n_kt) sstore(cur ^ 1);
+  // ---- prologue: tiles 0 and 1 resident, scores of tile 0 ----
+  load_k(0, 0);
+  load_v(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  store_v(0);
+  if (n_kt > 1) {
+    load_k(1, 1);
+    load_v(1);
+    __builtin_amdgcn_s_waitcnt(0);
+    store_v(1);
+  }
+  __syncthreads();
+
+  f32x16 s_a[2], s_b[2];
+  if (needs(0)) scores(0, s_a);
+
+  // One step: prefetch tile kt+2, scores of kt+1 (into s_next), softmax+PV of kt.
+  auto step = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_next)[2]) {
+    const int st_cur = kt % kStages;
+    const int st_nxt = (kt + 1) % kStages;
+    const int st_pre = (kt + 2) % kStages;
+    const bool pre = kt + 2 < n_kt;
+    if (pre) {
+      load_k(kt + 2, st_pre);
+      load_v(kt + 2);
+    }
+    if (kt + 1 < n_kt && needs(kt + 1)) scores(st_nxt, s_next);
+    if (needs(kt)) softmax_pv(kt, st_cur, s_cur);
+    if (pre) {
+      __builtin_amdgcn_s_waitcnt(0);
+      store_v(st_pre);
+    }
     __syncthreads();
+  };
+  for (int kt = 0; kt < n_kt; kt += 2) {
+    step(kt, s_a, s_b);
+    if (kt + 1 < n_kt) step(kt + 1, s_b, s_a);
   }
 
   // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
-  l_run += __shfl_xor(l_run, 32);
+  l_run = pair_sum(l_run);
   const float inv = 1.0f / l_run;
   if (my_row < p.S) {
     f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
@@ -271,15 +348,30 @@ __global__ __launch_bounds__(BM * 2) void flash_fwd_kernel(AttnArgs p) {
   }
 }
 
-template <int HD, int BM>
+template <int HD, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(AttnArgs p) {
+  flash_fwd_body<HD, NW, CAUSAL>(p);
+}
+
+template <int HD, int NW>
 int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
+  constexpr int BM = 32 * NW;
   const int64_t n_qt = (p.S + BM - 1) / BM;
   const int64_t grid = n_qt * p.B * p.H;
   if (causal)
-    hipLaunchKernelGGL((flash_fwd_kernel<HD, BM, true>), dim3((unsigned)grid), dim3(BM * 2), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, true>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_kernel<HD, BM, false>), dim3((unsigned)grid), dim3(BM * 2), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, false>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
   return check_launch("tk_flash_attn_fwd");
+}
+
+// Query rows per workgroup: 256 (8 waves sharing each K/V tile) for long
+// sequences, fewer when S is short so no wave idles on padding rows.
+template <int HD>
+int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
+  if (p.S > 128) return launch_flash<HD, 8>(p, causal, st);
+  if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
+  return launch_flash<HD, 2>(p, causal, st);
 }
 
 }  // namespace
@@ -324,12 +416,10 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
   p.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);
   const bool c = causal != 0;
-  // 128-row tiles once there are enough of them to fill the chip; 64 below.
-  const bool big = ((seq + 127) / 128) * batch * heads >= 512;
   switch (head_dim) {
-    case 16: return big ? launch_flash<16, 128>(p, c, st) : launch_flash<16, 64>(p, c, st);
-    case 32: return big ? launch_flash<32, 128>(p, c, st) : launch_flash<32, 64>(p, c, st);
-    case 64: return big ? launch_flash<64, 128>(p, c, st) : launch_flash<64, 64>(p, c, st);
-    default: return big ? launch_flash<128, 128>(p, c, st) : launch_flash<128, 64>(p, c, st);
+    case 16: return dispatch_flash<16>(p, c, st);
+    case 32: return dispatch_flash<32>(p, c, st);
+    case 64: return dispatch_flash<64>(p, c, st);
+    default: return dispatch_flash<128>(p, c, st);
   }
 }
