@@ -124,6 +124,7 @@ GEMM_SHAPES = [
     (1000, 200, 72),     # ragged M, N, K
     (77, 300, 8),        # tiny K
     (130, 130, 136),
+    (4000, 2100, 128),   # persistent path (more tiles than resident blocks) with M/N tails
 ]
 
 

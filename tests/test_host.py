@@ -110,6 +110,20 @@ def test_library_exports_every_declared_symbol():
     assert lib.tk_version() == _lib.ABI_VERSION
 
 
+def test_every_kernel_has_a_launch_stub():
+    """A kernel template whose host-side instantiation fails leaves its launch
+    stub undefined (the library then fails to load on first use)."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    missing = [line for line in out.splitlines() if " U " in line and "device_stub" in line]
+    assert not missing, missing[:5]
+
+
 def test_capability_probes():
     lib = _lib.load()
     assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256)] == [0, 1, 1, 1, 1, 0]

@@ -10,14 +10,16 @@
 // and LayerNorm epilogues then work on 16-byte (fp32) / 8-byte (fp16)
 // vectors along the row.
 //
-// Block tile BM x BN, K-step 64, two LDS stages.  Tiles are stored in LDS as
-// 128-byte rows of eight 16-byte chunks with the chunk index XOR-swizzled by
-// (row & 7), so both the row-wise global->LDS writes and the column-wise
-// fragment reads (32 rows, same chunk) are bank-conflict free.  The next
-// K-tile is fetched into registers while the current one feeds the MFMAs.
-// Block ids are remapped so that the tiles of one XCD (workgroups are dealt
-// round-robin over the 8 XCDs) form a compact group of output tiles sharing
-// A rows and W rows in that XCD's L2.
+// Block tile BM x BN (256x256 with 8 waves, 128x128 with 4, 64x64 with 1),
+// K-step BK with STAGES LDS buffers.  When K is a multiple of BK the K-tiles
+// are copied global -> LDS with global_load_lds_dwordx4 (no register
+// staging), STAGES-1 tiles in flight, one vmcnt wait + barrier per K-step;
+// otherwise a register-staged path with zero fill handles the K tail.  LDS
+// rows are XOR-swizzled per 256-byte bank line, so the fragment reads and
+// the copies are bank-conflict free on gfx950's 64-bank LDS.  Block ids are
+// remapped so that the tiles of one XCD (workgroups are dealt round-robin
+// over the 8 XCDs) form a compact group of output tiles sharing A rows and
+// W rows in that XCD's L2.
 #include "tk_common.hpp"
 
 namespace tk {
@@ -77,10 +79,9 @@ __device__ __forceinline__ void lds_barrier() {
 // Maps the hardware block id to an output tile (tm, tn).  Consecutive
 // hardware ids go to different XCDs; the remap gives each XCD a contiguous
 // run of logical ids, and logical ids walk GROUP_M tile-rows at a time.
-__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_of_block(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int kXcd = 8, kGroupM = 8;
   const int nb = tiles_m * tiles_n;
-  int id = blockIdx.x;
   const int full = nb - nb % kXcd;
   if (id < full) id = (id % kXcd) * (full / kXcd) + id / kXcd;
   const int per_group = kGroupM * tiles_n;
@@ -104,7 +105,7 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& tm,
 // copies, then one barrier.
 // Staged (K tail): 16-byte register prefetch of the next tile with zero fill
 // past M, N, K, two LDS buffers.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT, int SCHED = 1>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT>
 struct Mainloop {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = 64 * NW;
@@ -237,49 +238,10 @@ struct Mainloop {
     for (int kt = 0; kt < nk; ++kt) {
       const bool more = kt + STAGES - 1 < nk;
       const int nxt = cur == 0 ? STAGES - 1 : cur - 1;  // (kt + STAGES - 1) % STAGES
-      if (!(DIRECT && SCHED == 1) && more) issue(kt + STAGES - 1, nxt);
+      if (more) issue(kt + STAGES - 1, nxt);
       const f16* a_s = As + cur * BM * BK;
       const f16* w_s = Ws + cur * BN * BK;
-      if constexpr (DIRECT && SCHED == 1) {
-        // Fragments of step kk+1 are read while step kk's MFMAs run, and the
-        // next tile's copies are spread over the steps, so no step starts
-        // with a burst of memory instructions ahead of its MFMAs.
-        f16x8 fa[2][FM], fw[2][FN];
-        auto frags = [&](int buf, int kk) {
-          const int ch = 2 * kk + fhalf;
-#pragma unroll
-          for (int j = 0; j < FM; ++j)
-            fa[buf][j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
-#pragma unroll
-          for (int i = 0; i < FN; ++i)
-            fw[buf][i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
-        };
-        frags(0, 0);
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          if (kk + 1 < KSTEPS) frags((kk + 1) & 1, kk + 1);
-          if (more) {
-            f16* a_n = As + nxt * BM * BK;
-            f16* w_n = Ws + nxt * BN * BK;
-            const int kn = (kt + STAGES - 1) * BK;
-#pragma unroll
-            for (int i = 0; i < A_INSTS; ++i)
-              if (i % KSTEPS == kk)
-                __builtin_amdgcn_global_load_lds(ga[i] + kn, (lds_void*)(a_n + (wave * A_INSTS + i) * RPC * BK),
-                                                 16, 0, 0);
-#pragma unroll
-            for (int i = 0; i < W_INSTS; ++i)
-              if ((A_INSTS + i) % KSTEPS == kk)
-                __builtin_amdgcn_global_load_lds(gw[i] + kn, (lds_void*)(w_n + (wave * W_INSTS + i) * RPC * BK),
-                                                 16, 0, 0);
-          }
-#pragma unroll
-          for (int i = 0; i < FN; ++i)
-#pragma unroll
-            for (int j = 0; j < FM; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[kk & 1][i], fa[kk & 1][j], acc[i][j], 0, 0, 0);
-        }
-      } else {
+      {
 #pragma unroll
         for (int kk = 0; kk < KSTEPS; ++kk) {
           const int ch = 2 * kk + fhalf;
@@ -317,34 +279,24 @@ struct Mainloop {
 // Tile configuration: block tile BM x BN, wave grid WAVES_M x WAVES_N, and
 // for the direct-copy path the K step and number of LDS stages.  The staged
 // (K-tail) path always runs K step 64 with two stages.
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_, int SCHED_ = 1>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int BK = BK_, STAGES = STAGES_;
   static constexpr int NT = 64 * WAVES_M_ * WAVES_N_;
   template <bool DIRECT>
-  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT, SCHED_>;
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT>;
 };
 
-template <class T, int EPI, bool DIRECT>
-__global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
-  constexpr int BM = T::BM, BN = T::BN, WAVES_M = T::WAVES_M;
-  using ML = typename T::template ML<DIRECT>;
-  __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
-  const int tiles_m = (p.M + BM - 1) / BM;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  int tm, tn;
-  tile_of_block(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  f32x16 acc[ML::FN][ML::FM];
-  ML::run(p, m0, n0, smem, acc);
-
+// Epilogue of one output tile: bias (+ GELU) to fp16, or bias + fp32
+// residual to fp32, with 4-wide vector stores where the row layout allows.
+template <class ML, int WAVES_M, int EPI>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
+                                           int n0) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m_w = m0 + (wave % WAVES_M) * ML::WM + (lane & 31);
   const int n_w = n0 + (wave / WAVES_M) * ML::WN + 4 * (lane >> 5);
-
 #pragma unroll
   for (int i = 0; i < ML::FN; ++i) {
 #pragma unroll
@@ -388,6 +340,20 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   }
 }
 
+template <class T, int EPI, bool DIRECT>
+__global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
+  constexpr int BM = T::BM, BN = T::BN;
+  using ML = typename T::template ML<DIRECT>;
+  __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  f32x16 acc[ML::FN][ML::FM];
+  ML::run(p, tm * BM, tn * BN, smem, acc);
+  store_tile<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN);
+}
+
 // Full-row variant: BN == N, so each block owns complete output rows and
 // finishes the residual add + LayerNorm + cast before anything leaves the
 // chip.  Row statistics: per-lane partial sums over its n values, the
@@ -402,7 +368,7 @@ __global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
   __shared__ float red[WAVES_N][BM];
   const int tiles_m = (p.M + BM - 1) / BM;
   int tm, tn;
-  tile_of_block(tiles_m, 1, tm, tn);
+  tile_of_block(blockIdx.x, tiles_m, 1, tm, tn);
   const int m0 = tm * BM;
 
   f32x16 acc[ML::FN][ML::FM];
@@ -508,10 +474,11 @@ template <class T, int EPI>
 int launch_gemm(const GemmArgs& p, hipStream_t st) {
   const int64_t tiles = (int64_t)((p.M + T::BM - 1) / T::BM) * ((p.N + T::BN - 1) / T::BN);
   // The direct global->LDS copy needs whole K tiles.
-  if (p.K % T::BK == 0)
+  if (p.K % T::BK == 0) {
     hipLaunchKernelGGL((gemm_kernel<T, EPI, true>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
-  else
+  } else {
     hipLaunchKernelGGL((gemm_kernel<T, EPI, false>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
+  }
   return check_launch("tk_gemm");
 }
 
