@@ -115,16 +115,19 @@ def test_layernorm_model_widths_no_sum(cols):
 # GEMM + epilogues
 # --------------------------------------------------------------------------- #
 
-GEMM_SHAPES = [
-    (512, 384, 128),     # C1 QKV (reduced M)
-    (1024, 1536, 512),   # C2 QKV
-    (1024, 512, 2048),   # C2 FFN-down
-    (4096, 4096, 1024),  # large-tile path (256x256 tiles)
-    (4096, 2048, 8192),  # C4 FFN-down (reduced M), long K
-    (1000, 200, 72),     # ragged M, N, K
-    (77, 300, 8),        # tiny K
+GEMM_SHAPES = [  # one or more per tile configuration of the dispatch, direct and K-tail paths
+    (512, 384, 128),      # C1 QKV (reduced M): 64x64 tiles
+    (1024, 1536, 512),    # C2 QKV (reduced M)
+    (1024, 512, 2048),    # C2 FFN-down (reduced M)
+    (4096, 4096, 1024),   # 256x256 tiles
+    (4096, 2048, 8192),   # C4 FFN-down (reduced M), long K: 128x128 tiles
+    (1000, 200, 72),      # ragged M, N, K
+    (77, 300, 8),         # tiny K
     (130, 130, 136),
-    (4000, 2100, 128),   # persistent path (more tiles than resident blocks) with M/N tails
+    (4000, 2100, 128),    # 128x128 tiles with M and N tails
+    (12800, 512, 2048),   # 256x128 tiles, three K stages
+    (13000, 500, 2056),   # 256x128 tiles, K tail, M and N tails
+    (4100, 4200, 1032),   # 256x256 tiles, K tail, M and N tails
 ]
 
 
@@ -147,7 +150,7 @@ def test_gemm_bias_and_gelu(m, n, k, gelu):
     torch.testing.assert_close(got.cpu().float(), ref.half().float(), atol=1e-3, rtol=1e-3)
 
 
-@pytest.mark.parametrize("m,n,k", GEMM_SHAPES[:6])
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
 def test_gemm_residual_inplace(m, n, k):
     a, w, bias, ref = _gemm_inputs(m, n, k, seed=3)
     resid = seeded(m, n, seed=9)

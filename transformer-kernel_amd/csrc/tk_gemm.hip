@@ -40,7 +40,8 @@ struct GemmArgs {
   int64_t lda, ldw, ldr, ldc;
   int M, N, K;
   float eps;
-  bool vec;  // output rows admit 4-wide vector stores
+  bool vec;     // output rows admit 4-wide vector stores
+  bool bias16;  // bias is 16-byte aligned
 };
 
 // LDS tile layout: rows of BK halves (BK = 64: 128 bytes = eight 16-byte
@@ -92,6 +93,11 @@ __device__ __forceinline__ void tile_of_block(int id, int tiles_m, int tiles_n, 
   tn = in_group / gsize;
 }
 
+// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+}
+
 // Main loop: accumulates the (BN x BM) transposed tile into acc.
 // Wave (wm, wn) owns rows n in [wn*WN, +WN) and m in [wm*WM, +WM) of the tile.
 //
@@ -100,9 +106,13 @@ __device__ __forceinline__ void tile_of_block(int id, int tiles_m, int tiles_n, 
 // LDS in lane order; lane l covers tile row r0 + l / (chunks per row) and
 // physical chunk l % (chunks per row), and fetches the logical chunk the
 // swizzle puts there.  Rows past M / N re-read the last valid row (their
-// outputs are never stored).  STAGES LDS buffers keep STAGES-1 tiles in
-// flight; after each tile the wave waits (vmcnt) only for the next tile's
-// copies, then one barrier.
+// outputs are never stored).  All STAGES buffers are filled up front; after
+// K-tile t has been read into registers, a wave waits (vmcnt) only for tile
+// t+1's copies, one barrier, and the freed buffer starts receiving tile
+// t+STAGES.  Fragments are double-buffered in registers: the reads of k-step
+// s+1 are issued between the MFMAs of k-step s, and the first reads of the
+// next K-tile are issued before the MFMAs of the current tile's last k-step,
+// so the matrix cores keep working across the barrier.
 // Staged (K tail): 16-byte register prefetch of the next tile with zero fill
 // past M, N, K, two LDS buffers.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT>
@@ -120,154 +130,203 @@ struct Mainloop {
   static constexpr int A_INSTS = BM / RPC / NW;  // direct: wave copies per tile
   static constexpr int W_INSTS = BN / RPC / NW;
   static constexpr int INSTS = A_INSTS + W_INSTS;
+  static constexpr int KSTEPS = BK / 16;
   static constexpr int LDS_HALVES = STAGES * (BM + BN) * BK;
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
+  static_assert(KSTEPS % 2 == 0, "even number of k-steps per K-tile");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(DIRECT || STAGES == 2, "the staged path double-buffers");
   static_assert(!DIRECT || (BM % (RPC * NW) == 0 && BN % (RPC * NW) == 0), "copies must divide waves");
   static_assert(DIRECT || ((BM * CPR) % NT == 0 && (BN * CPR) % NT == 0), "chunks must divide threads");
-  static_assert((STAGES - 2) * INSTS < 64, "vmcnt range");
+  static_assert((STAGES - 1) * INSTS < 64, "vmcnt range");
 
-  __device__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave % WAVES_M;
-    const int wn = wave / WAVES_M;
-    f16* As = smem;                      // [STAGES][BM][BK]
-    f16* Ws = smem + STAGES * BM * BK;   // [STAGES][BN][BK]
-
+  __device__ static void zero(f32x16 (&acc)[FN][FM]) {
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int j = 0; j < FM; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
 
-    const int nk = (p.K + BK - 1) / BK;
+  __device__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+    zero(acc);
+    if constexpr (DIRECT) run_direct(p, m0, n0, smem, acc);
+    else run_staged(p, m0, n0, smem, acc);
+  }
 
-    const f16* ga[DIRECT ? A_INSTS : 1];
-    const f16* gw[DIRECT ? W_INSTS : 1];
-    f16x8 ra[DIRECT ? 1 : A_LOADS], rw[DIRECT ? 1 : W_LOADS];
+  __device__ static void run_direct(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave % WAVES_M;
+    const int wn = wave / WAVES_M;
+    f16* As = smem;                      // [STAGES][BM][BK]
+    f16* Ws = smem + STAGES * BM * BK;   // [STAGES][BN][BK]
+    const int nk = p.K / BK;
 
-    if constexpr (DIRECT) {
+    const f16* ga[A_INSTS];
+    const f16* gw[W_INSTS];
 #pragma unroll
-      for (int i = 0; i < A_INSTS; ++i) {
-        const int r = (wave * A_INSTS + i) * RPC + lane / CPR;
-        const int c = swz<BK>(r, lane % CPR) - r * BK;  // physical -> logical is the same XOR
-        ga[i] = p.a + (int64_t)min(m0 + r, p.M - 1) * p.lda + c;
-      }
-#pragma unroll
-      for (int i = 0; i < W_INSTS; ++i) {
-        const int r = (wave * W_INSTS + i) * RPC + lane / CPR;
-        const int c = swz<BK>(r, lane % CPR) - r * BK;
-        gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
-      }
+    for (int i = 0; i < A_INSTS; ++i) {
+      const int r = (wave * A_INSTS + i) * RPC + lane / CPR;
+      const int c = swz<BK>(r, lane % CPR) - r * BK;  // physical -> logical is the same XOR
+      ga[i] = p.a + (int64_t)min(m0 + r, p.M - 1) * p.lda + c;
     }
-
+#pragma unroll
+    for (int i = 0; i < W_INSTS; ++i) {
+      const int r = (wave * W_INSTS + i) * RPC + lane / CPR;
+      const int c = swz<BK>(r, lane % CPR) - r * BK;
+      gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
+    }
     auto issue = [&](int kt, int stage) {  // start tile kt's copy into `stage`
-      if constexpr (DIRECT) {
-        f16* a_s = As + stage * BM * BK;
-        f16* w_s = Ws + stage * BN * BK;
+      f16* a_s = As + stage * BM * BK;
+      f16* w_s = Ws + stage * BN * BK;
 #pragma unroll
-        for (int i = 0; i < A_INSTS; ++i)
-          __builtin_amdgcn_global_load_lds(ga[i] + kt * BK,
-                                           (lds_void*)(a_s + (wave * A_INSTS + i) * RPC * BK), 16, 0, 0);
+      for (int i = 0; i < A_INSTS; ++i)
+        __builtin_amdgcn_global_load_lds(ga[i] + kt * BK, (lds_void*)(a_s + (wave * A_INSTS + i) * RPC * BK),
+                                         16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < W_INSTS; ++i)
-          __builtin_amdgcn_global_load_lds(gw[i] + kt * BK,
-                                           (lds_void*)(w_s + (wave * W_INSTS + i) * RPC * BK), 16, 0, 0);
-      } else {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-          const int idx = tid + i * NT;
-          const int row = idx / CPR, ch = idx % CPR;
-          const int gm = m0 + row, gk = k0 + ch * 8;
-          if (gm < p.M && gk < p.K)
-            ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
-          else
-            ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < W_LOADS; ++i) {
-          const int idx = tid + i * NT;
-          const int row = idx / CPR, ch = idx % CPR;
-          const int gn = n0 + row, gk = k0 + ch * 8;
-          if (gn < p.N && gk < p.K)
-            rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
-          else
-            rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-      }
+      for (int i = 0; i < W_INSTS; ++i)
+        __builtin_amdgcn_global_load_lds(gw[i] + kt * BK, (lds_void*)(w_s + (wave * W_INSTS + i) * RPC * BK),
+                                         16, 0, 0);
     };
-    auto land = [&](int stage) {  // staged path: registers -> LDS
-      if constexpr (!DIRECT) {
-        f16* a_s = As + stage * BM * BK;
-        f16* w_s = Ws + stage * BN * BK;
+    const int frow = lane & 31;   // fragment row within a 32-row block
+    const int fhalf = lane >> 5;  // which 8-wide k half of a 16-wide k step
+    f16x8 fa[2][FM], fw[2][FN];
+    auto read = [&](int b, int stage, int kk) {
+      const f16* a_s = As + stage * BM * BK;
+      const f16* w_s = Ws + stage * BN * BK;
+      const int ch = 2 * kk + fhalf;
 #pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-          const int idx = tid + i * NT;
-          *reinterpret_cast<f16x8*>(a_s + swz<BK>(idx / CPR, idx % CPR)) = ra[i];
-        }
+      for (int j = 0; j < FM; ++j)
+        fa[b][j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
 #pragma unroll
-        for (int i = 0; i < W_LOADS; ++i) {
-          const int idx = tid + i * NT;
-          *reinterpret_cast<f16x8*>(w_s + swz<BK>(idx / CPR, idx % CPR)) = rw[i];
-        }
+      for (int i = 0; i < FN; ++i)
+        fw[b][i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
+    };
+    auto mma = [&](int b) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+    };
+    // Scheduling hint for one k-step: one fragment read after each of the
+    // first FM + FN MFMAs, then the remaining MFMAs.
+    auto interleave = [&]() {
+#pragma unroll
+      for (int x = 0; x < FM + FN; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
       }
+      if constexpr (FM * FN > FM + FN) __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - FM - FN, 0);
     };
 
-    if constexpr (DIRECT) {
 #pragma unroll
-      for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nk) issue(s, s);
-      if (nk >= STAGES - 1) wait_vmcnt<(STAGES - 2) * INSTS>();
-      else wait_vmcnt<0>();
-      lds_barrier();
-    } else {
-      issue(0, 0);
-      land(0);
-      __syncthreads();
-    }
-
-    const int frow = lane & 31;  // fragment row within a 32-row block
-    const int fhalf = lane >> 5; // which 8-wide k half of a 16-wide k step
+    for (int s = 0; s < STAGES; ++s)
+      if (s < nk) issue(s, s);
+    if (nk >= STAGES) wait_vmcnt<(STAGES - 1) * INSTS>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    read(0, 0, 0);
     int cur = 0;
-    constexpr int KSTEPS = BK / 16;
     for (int kt = 0; kt < nk; ++kt) {
-      const bool more = kt + STAGES - 1 < nk;
-      const int nxt = cur == 0 ? STAGES - 1 : cur - 1;  // (kt + STAGES - 1) % STAGES
-      if (more) issue(kt + STAGES - 1, nxt);
-      const f16* a_s = As + cur * BM * BK;
-      const f16* w_s = Ws + cur * BN * BK;
-      {
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const int ch = 2 * kk + fhalf;
-          f16x8 fa[FM], fw[FN];
-#pragma unroll
-          for (int j = 0; j < FM; ++j)
-            fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
-#pragma unroll
-          for (int i = 0; i < FN; ++i)
-            fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
-#pragma unroll
-          for (int i = 0; i < FN; ++i)
-#pragma unroll
-            for (int j = 0; j < FM; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
-        }
+      for (int kk = 0; kk < KSTEPS - 1; ++kk) {
+        read((kk + 1) & 1, cur, kk + 1);
+        mma(kk & 1);
+        interleave();
       }
-      if constexpr (DIRECT) {
-        if (more) wait_vmcnt<(STAGES - 2) * INSTS>();
+      if (kt + 1 < nk) {
+        wait_lgkm0();  // this K-tile's fragments are all in registers
+        if (kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * INSTS>();
         else wait_vmcnt<0>();
         lds_barrier();
-      } else {
-        if (more) land(cur ^ 1);
-        __syncthreads();
+        if (kt + STAGES < nk) issue(kt + STAGES, cur);
+        cur = cur + 1 == STAGES ? 0 : cur + 1;
+        read(0, cur, 0);
       }
-      cur = cur + 1 == STAGES ? 0 : cur + 1;
+      mma(1);
+    }
+  }
+
+  __device__ static void run_staged(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % WAVES_M;
+    const int wn = wave / WAVES_M;
+    f16* As = smem;
+    f16* Ws = smem + 2 * BM * BK;
+    const int nk = (p.K + BK - 1) / BK;
+    f16x8 ra[A_LOADS], rw[W_LOADS];
+    auto fetch = [&](int kt) {
+      const int k0 = kt * BK;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        const int row = idx / CPR, ch = idx % CPR;
+        const int gm = m0 + row, gk = k0 + ch * 8;
+        if (gm < p.M && gk < p.K)
+          ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
+        else
+          ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < W_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        const int row = idx / CPR, ch = idx % CPR;
+        const int gn = n0 + row, gk = k0 + ch * 8;
+        if (gn < p.N && gk < p.K)
+          rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
+        else
+          rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    };
+    auto land = [&](int stage) {
+      f16* a_s = As + stage * BM * BK;
+      f16* w_s = Ws + stage * BN * BK;
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        *reinterpret_cast<f16x8*>(a_s + swz<BK>(idx / CPR, idx % CPR)) = ra[i];
+      }
+#pragma unroll
+      for (int i = 0; i < W_LOADS; ++i) {
+        const int idx = tid + i * NT;
+        *reinterpret_cast<f16x8*>(w_s + swz<BK>(idx / CPR, idx % CPR)) = rw[i];
+      }
+    };
+    fetch(0);
+    land(0);
+    __syncthreads();
+    const int frow = lane & 31;
+    const int fhalf = lane >> 5;
+    int cur = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const bool more = kt + 1 < nk;
+      if (more) fetch(kt + 1);
+      const f16* a_s = As + cur * BM * BK;
+      const f16* w_s = Ws + cur * BN * BK;
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const int ch = 2 * kk + fhalf;
+        f16x8 fa[FM], fw[FN];
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          fa[j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          fw[i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[i], fa[j], acc[i][j], 0, 0, 0);
+      }
+      if (more) land(cur ^ 1);
+      __syncthreads();
+      cur ^= 1;
     }
   }
 };
@@ -288,55 +347,122 @@ struct Tile {
   using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT>;
 };
 
-// Epilogue of one output tile: bias (+ GELU) to fp16, or bias + fp32
-// residual to fp32, with 4-wide vector stores where the row layout allows.
+// Byte offset of 16-byte chunk `chunk` of row `row` in a row-major LDS
+// staging region with CPR chunks per row: the chunk index is XOR-ed with the
+// row's position inside its 256-byte bank line group, so that 16 rows written
+// at one logical chunk, and the rows read back 16 bytes per lane, each hit
+// distinct banks.
+template <int CPR>
+__device__ __forceinline__ int epi_off(int row, int chunk) {
+  int f;
+  if constexpr (CPR >= 16) f = row & 15;
+  else f = (row / (16 / CPR)) % CPR;
+  return row * CPR * 16 + ((chunk ^ f) << 4);
+}
+
+// Each wave stages its WM x WN result tile (in rows of 32 x JC) in its own LDS
+// region, row-major, then reads it back 16 bytes per lane along rows: every
+// global store, and every fp32 residual load, then covers whole 128-byte
+// lines instead of 16-byte pieces of 32 rows.  Bias and GELU are applied in
+// fp32 before the fp16 rounding; the fp32 residual epilogue adds bias and
+// residual on the read-back side.
 template <class ML, int WAVES_M, int EPI>
-__device__ __forceinline__ void store_tile(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
-                                           int n0) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int m_w = m0 + (wave % WAVES_M) * ML::WM + (lane & 31);
-  const int n_w = n0 + (wave / WAVES_M) * ML::WN + 4 * (lane >> 5);
+__device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
+                                               int n0, f16* smem) {
+  constexpr bool F32 = EPI == TK_EPI_BIAS_RESID;
+  constexpr int ES = F32 ? 4 : 2;
+  constexpr int WM = ML::WM, WN = ML::WN, FM = ML::FM, FN = ML::FN, NW = ML::NW;
+  constexpr int ROWB = WN * ES;
+  constexpr int CPR = ROWB / 16;
+  constexpr int LDS_BYTES = ML::LDS_HALVES * 2;
+  constexpr int JC = (NW * FM * 32 * ROWB <= LDS_BYTES) ? FM : (NW * 32 * ROWB <= LDS_BYTES ? 1 : 0);
+  static_assert(JC > 0 && FM % JC == 0, "staging region does not fit");
+  constexpr int EPC = 16 / ES;  // elements per chunk
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int mw = m0 + (wave % WAVES_M) * WM;
+  const int nw = n0 + (wave / WAVES_M) * WN;
+  char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
+  __syncthreads();  // every wave is done with the main-loop buffers
 #pragma unroll
-  for (int i = 0; i < ML::FN; ++i) {
+  for (int jb = 0; jb < FM; jb += JC) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = n_w + i * 32 + 8 * q;
-      if (n >= p.N) continue;
-      const bool full = p.vec && n + 3 < p.N;
-      float bv[4];
+    for (int i = 0; i < FN; ++i) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bv[e] = (p.bias && n + e < p.N) ? p.bias[n + e] : 0.f;
+      for (int q = 0; q < 4; ++q) {
+        const int nl = i * 32 + 8 * q + 4 * (lane >> 5);  // 4 consecutive n of this lane
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (!F32) {
+          const int n = nw + nl;
+          if (p.bias) {
+            if (p.bias16 && n + 3 < p.N) {
+              const f32x4 b4 = *reinterpret_cast<const f32x4*>(p.bias + n);
+              bv[0] = b4[0]; bv[1] = b4[1]; bv[2] = b4[2]; bv[3] = b4[3];
+            } else {
 #pragma unroll
-      for (int j = 0; j < ML::FM; ++j) {
-        const int m = m_w + j * 32;
-        if (m >= p.M) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e] + bv[e];
-        if constexpr (EPI == TK_EPI_BIAS_RESID) {
-          const float* rr = p.resid + (int64_t)m * p.ldr + n;
-          float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
-          if (full) {
-            const f32x4 r = *reinterpret_cast<const f32x4*>(rr);
-            *reinterpret_cast<f32x4*>(cr) = f32x4{r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
-          } else {
-            for (int e = 0; e < 4 && n + e < p.N; ++e) cr[e] = rr[e] + v[e];
+              for (int e = 0; e < 4; ++e) bv[e] = n + e < p.N ? p.bias[n + e] : 0.f;
+            }
           }
-        } else {
-          if constexpr (EPI == TK_EPI_BIAS_GELU) {
+        }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-          }
-          f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
-          if (full) {
-            *reinterpret_cast<f16x4*>(cr) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        for (int jj = 0; jj < JC; ++jj) {
+          const int row = jj * 32 + (lane & 31);
+          const f32x16& a = acc[i][jb + jj];
+          if constexpr (F32) {
+            *reinterpret_cast<f32x4*>(region + epi_off<CPR>(row, nl / 4)) =
+                f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
           } else {
-            for (int e = 0; e < 4 && n + e < p.N; ++e) cr[e] = (f16)v[e];
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = a[4 * q + e] + bv[e];
+              if constexpr (EPI == TK_EPI_BIAS_GELU) v[e] = gelu_erf(v[e]);
+            }
+            *reinterpret_cast<f16x4*>(region + epi_off<CPR>(row, nl / 8) + (nl % 8) * 2) =
+                f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
           }
         }
       }
     }
+    asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
+    constexpr int TOT = JC * 32 * CPR;
+    static_assert(TOT % 64 == 0, "whole read-back passes");
+#pragma unroll
+    for (int idx0 = 0; idx0 < TOT; idx0 += 64) {
+      const int idx = idx0 + lane;
+      const int row = idx / CPR, ch = idx % CPR;
+      const int m = mw + jb * 32 + row;
+      const int n = nw + ch * EPC;
+      const char* src = region + epi_off<CPR>(row, ch);
+      if (m < p.M && n < p.N) {
+        if constexpr (F32) {
+          const f32x4 d = *reinterpret_cast<const f32x4*>(src);
+          const float* rr = p.resid + (int64_t)m * p.ldr + n;
+          float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
+          if (p.vec && n + 3 < p.N) {
+            const f32x4 r = *reinterpret_cast<const f32x4*>(rr);
+            f32x4 b = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias) {
+              if (p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
+              else b = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
+            }
+            *reinterpret_cast<f32x4*>(cr) = f32x4{r[0] + (d[0] + b[0]), r[1] + (d[1] + b[1]),
+                                                  r[2] + (d[2] + b[2]), r[3] + (d[3] + b[3])};
+          } else {
+            for (int e = 0; e < 4 && n + e < p.N; ++e)
+              cr[e] = rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f));
+          }
+        } else {
+          const f16x8 d = *reinterpret_cast<const f16x8*>(src);
+          f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
+          if (p.vec && n + 7 < p.N) {
+            *reinterpret_cast<f16x8*>(cr) = d;
+          } else {
+            for (int e = 0; e < 8 && n + e < p.N; ++e) cr[e] = d[e];
+          }
+        }
+      }
+    }
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -351,7 +477,7 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   f32x16 acc[ML::FN][ML::FM];
   ML::run(p, tm * BM, tn * BN, smem, acc);
-  store_tile<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN);
+  store_tile_lds<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem);
 }
 
 // Full-row variant: BN == N, so each block owns complete output rows and
@@ -483,18 +609,21 @@ int launch_gemm(const GemmArgs& p, hipStream_t st) {
 }
 
 using TileBig = Tile<256, 256, 4, 2, 64, 2>;   // 8 waves of 64 x 128
+using TileWide = Tile<256, 128, 2, 2, 64, 3>;  // 4 waves of 128 x 64, three K stages
 using TileMid = Tile<128, 128, 2, 2, 64, 2>;   // 4 waves of 64 x 64, 2 blocks per CU
 using TileSmall = Tile<64, 64, 1, 1, 64, 2>;   // 1 wave
 
 template <int EPI>
 int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const int64_t t256x128 = (int64_t)((p.M + 255) / 256) * ((p.N + 127) / 128);
   const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  // Measured on MI355X: 256x256 tiles win only once K is long enough to
-  // amortise their prologue/epilogue (K >= 4096) and they fill the 256 CUs;
-  // 128x128 (2 blocks per CU) wins for shorter K; 64x64 for the small,
-  // launch-bound shapes.
-  if (p.K >= 4096 && t256 >= 240) return launch_gemm<TileBig, EPI>(p, st);
+  // Measured on MI355X (fp16, 256 CUs): 256x256 tiles win once there is at
+  // least one full round of them; narrow outputs (N <= 512) with long K
+  // prefer 256x128 with three K stages, short K the 128x128 tile (two
+  // blocks per CU); 64x64 for the small, launch-bound shapes.
+  if (p.N <= 512 && p.K >= 2048 && t256x128 >= 200) return launch_gemm<TileWide, EPI>(p, st);
+  if (p.N > 512 && t256 >= 256) return launch_gemm<TileBig, EPI>(p, st);
   if (t128 >= 200) return launch_gemm<TileMid, EPI>(p, st);
   return launch_gemm<TileSmall, EPI>(p, st);
 }
@@ -537,12 +666,13 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
     TK_REQUIRE(resid != nullptr && ldr >= n, TK_ERR_ARG, "tk_gemm: residual epilogue needs resid, ldr >= n");
   if (m == 0 || n == 0) return TK_OK;
   GemmArgs p{};
-  // 4-wide vector stores (and residual loads) when every output row start is
-  // aligned for them; element-wise otherwise.
+  // 16-byte vector stores (and residual loads) when every output row start
+  // is aligned for them; element-wise otherwise.
   if (epilogue == TK_EPI_BIAS_RESID)
     p.vec = aligned16(resid) && aligned16(c) && ldr % 4 == 0 && ldc % 4 == 0;
   else
-    p.vec = ((uintptr_t)c & 7) == 0 && ldc % 4 == 0;
+    p.vec = aligned16(c) && ldc % 8 == 0;
+  p.bias16 = bias != nullptr && aligned16(bias);
   p.a = reinterpret_cast<const f16*>(a);
   p.w = reinterpret_cast<const f16*>(w);
   p.bias = bias;
