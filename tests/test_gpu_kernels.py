@@ -251,6 +251,48 @@ def test_flash_attention_ragged_sequence_lengths(s):
         assert bad == 0, (causal, err)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("s", [512, 600, 777, 1000, 1300])
+def test_flash_attention_long_ragged(s, hd):
+    """Long sequences (the two-group kernel): lengths off the 64-key tile and
+    256-row block grid, causal and full."""
+    b, h = 1, 2
+    q, k, v = _qkv((b, h, s, hd), seed=s + hd)
+    for causal in (True, False):
+        out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_attention_long_strided_views(hd):
+    """q/k/v as strided views of one fused [B, S, 3, H, hd] projection, as the model passes them."""
+    b, h, s = 2, 3, 1100
+    qkv = seeded(b, s, 3, h, hd, dtype=torch.float16, seed=7)
+    q, k, v = qkv.to(DEV).permute(2, 0, 3, 1, 4).unbind(0)
+    qc, kc, vc = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    for causal in (True, False):
+        out = ops.flash_attention(q, k, v, hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(qc, kc, vc, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_attention_large_logits(hd):
+    """Scores spanning many powers of two: the running max moves often (rescale path)
+    and most probabilities underflow."""
+    b, h, s = 1, 2, 1024
+    q, k, v = _qkv((b, h, s, hd), seed=99)
+    # growing query norms along the sequence -> the row max jumps across tiles
+    ramp = torch.linspace(0.5, 6.0, s).view(1, 1, s, 1)
+    q = (q.float() * ramp).half()
+    k = (k.float() * 2.0).half()
+    for causal in (True, False):
+        out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+
+
 def test_attention_support_probes():
     assert ops.attention_supported(64, torch.float16, DEV)
     assert not ops.attention_supported(8, torch.float16, DEV)
