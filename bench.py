@@ -89,6 +89,32 @@ def kernel_units(name: str, cfg) -> tuple:
     raise KeyError(name)
 
 
+COPY_BYTES = 512 * 1024 * 1024  # per direction
+
+
+def copy_calibration() -> int:
+    """Ten plain copies of COPY_BYTES (read COPY_BYTES, write COPY_BYTES each)."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_direction": COPY_BYTES, "launches": 10}), flush=True)
+    return 0
+
+
+def measured_traffic(config: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` at ``config`` from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE summary (profiles/traffic.json), or None."""
+    path = REPO / "profiles" / "traffic.json"
+    try:
+        table = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = table.get("kernels", {}).get(config, {}).get(kernel)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -99,6 +125,9 @@ def main() -> int:
     ap.add_argument("--no-check", action="store_true", help="skip the one-trial parity check")
     ap.add_argument("--graph", action="store_true",
                     help="time the whole forward replayed from a HIP graph (tkmi.graphs.GraphedTransformer)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of COPY_BYTES (torch copy_), the reference kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -113,6 +142,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (MI355X)", file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration()
 
     import tkmi
     from tkmi import ops
@@ -209,7 +241,7 @@ def main() -> int:
         "peak": PEAK_FP16_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBPS,
         "unit": dom["unit"],
         "frac": dom["frac"],
-        "traffic": None,
+        "traffic": measured_traffic(args.config, dom_name),
     }
 
     cpu = None
