@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TKMI_ABI_VERSION 1
+#define TKMI_ABI_VERSION 2
 
 typedef uint16_t tk_half;
 
@@ -39,6 +39,19 @@ enum tk_status {
 };
 
 enum tk_dtype { TK_F32 = 0, TK_F16 = 1 };
+
+/*
+ * Padding masks.  `row_valid` arguments are nullable [rows] byte arrays
+ * (nonzero = valid token; a torch bool tensor's storage); NULL means every
+ * row is valid and the kernels take their unmasked path.  The row modes give
+ * what an invalid row of a residual update becomes, following the baseline
+ * block (src/torch_transformer_benchmark.py:119-120,141-142,170-171):
+ */
+enum tk_row_mode {
+  TK_ROWS_KEEP_RESID = 1, /* s = resid: the attention output of a padded row is 0 */
+  TK_ROWS_ZERO = 2,       /* s = 0: the block output of a padded row is 0           */
+  TK_ROWS_ZERO_ALL = 3    /* s = 0 and the normalised output h = 0 (final norm)     */
+};
 
 enum tk_epilogue {
   TK_EPI_BIAS = 0,      /* C(f16)  = A.W^T + bias                          */
@@ -56,13 +69,15 @@ const char *tk_last_error_string(void);
  * LayerNorm over the last dim + cast.
  *   out[r, :] = (x[r,:] - mean) * rsqrt(var_pop + eps) * w + b   (fp32 math)
  * x: [rows, cols] f32 contiguous; w, b: [cols] f32; out: [rows, cols] of
- * out_dtype (TK_F16 or TK_F32).  cols in [1, 8192].
+ * out_dtype (TK_F16 or TK_F32).  cols in [1, 8192].  row_valid (nullable):
+ * rows marked invalid are written as zeros (the final norm of a padded row,
+ * src/torch_transformer_benchmark.py:170-171).
  * Replaces fused_kernels.ln_fwd / _ln_kernel (src/fused_kernels.py:164-193,
  * :80-112).
  */
 int tk_ln_cast(const float *x, const float *w, const float *b, void *out,
                int out_dtype, int64_t rows, int64_t cols, float eps,
-               void *stream);
+               const uint8_t *row_valid, void *stream);
 
 /*
  * Residual add + LayerNorm + cast.
@@ -84,18 +99,23 @@ int tk_add_ln_cast(const float *x, const void *y, int y_dtype, const float *w,
  * epilogue TK_EPI_BIAS_RESID: C is f32 (ldc), resid is f32 (ldr), C may
  * equal resid (in-place residual stream update).
  * k must be a multiple of 8 and lda/ldw multiples of 8 (16-byte rows).
+ * row_valid / row_mode (TK_EPI_BIAS_RESID only; row_valid nullable, m bytes):
+ * an invalid row m is written as resid (TK_ROWS_KEEP_RESID) or 0
+ * (TK_ROWS_ZERO, TK_ROWS_ZERO_ALL).
  * Replaces torch F.linear (+ F.gelu) in src/optimized.py:572,627,632-636.
  */
 int tk_gemm(const tk_half *a, int64_t lda, const tk_half *w, int64_t ldw,
             const float *bias, const float *resid, int64_t ldr, void *c,
             int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
-            void *stream);
+            const uint8_t *row_valid, int row_mode, void *stream);
 
 /*
  * GEMM with the residual + LayerNorm + cast epilogue over full output rows:
  *   s = resid + A.W^T + bias (fp32);  h = LN(s; ln_w, ln_b, eps) -> h_dtype
  * sum_out (may be NULL, may alias resid) receives s.  Rows of n elements
  * must fit one tile: n in {128, 256, 512} (tk_gemm_ln_supported).
+ * row_valid (nullable, m bytes) / row_mode: an invalid row takes s per
+ * row_mode (tk_row_mode); h = LN(s), or 0 under TK_ROWS_ZERO_ALL.
  * Replaces F.linear followed by fused_kernels.add_ln_fwd
  * (src/optimized.py:523-553 with :627 / :636).
  */
@@ -103,7 +123,8 @@ int tk_gemm_bias_add_ln(const tk_half *a, int64_t lda, const tk_half *w,
                         int64_t ldw, const float *bias, const float *resid,
                         const float *ln_w, const float *ln_b, float *sum_out,
                         void *h_out, int h_dtype, int64_t m, int64_t n,
-                        int64_t k, float eps, void *stream);
+                        int64_t k, float eps, const uint8_t *row_valid,
+                        int row_mode, void *stream);
 
 /* 1 when tk_gemm_bias_add_ln handles rows of n elements, else 0. */
 int tk_gemm_ln_supported(int64_t n);
@@ -116,6 +137,11 @@ int tk_gemm_ln_supported(int64_t n);
  * {S*H*hd, hd, H*hd} for the [B, S, H*hd] layout).
  * scores = (q.k^T) * scale in fp32, causal masks key > query, fp32 softmax,
  * fp16 P on MFMA for P.V, fp32 accumulation.
+ * key_valid (nullable): key validity bytes, key s of batch b at
+ * key_valid[b * key_valid_stride + s]; invalid keys are masked with -inf
+ * like future keys (src/torch_transformer_benchmark.py:104-107).  A query
+ * row with no valid key yields non-finite output (the baseline's NaN row);
+ * callers zero such padded rows downstream.
  * head_dim in {16, 32, 64, 128} (tk_attention_supported).
  * Replaces kernels.flash_attention / _flash_attn_fwd_kernel
  * (src/kernels.py:250-294, :137-247) and F.scaled_dot_product_attention
@@ -126,6 +152,7 @@ int tk_flash_attn_fwd(const tk_half *q, const tk_half *k, const tk_half *v,
                       int64_t head_dim, const int64_t *q_strides,
                       const int64_t *k_strides, const int64_t *v_strides,
                       const int64_t *o_strides, float scale, int causal,
+                      const uint8_t *key_valid, int64_t key_valid_stride,
                       void *stream);
 
 /* 1 when tk_flash_attn_fwd handles head_dim, else 0.

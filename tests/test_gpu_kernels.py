@@ -66,6 +66,19 @@ def test_layernorm_fp32_out_is_tight():
     torch.testing.assert_close(y.cpu(), ref, atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("cols", [64, 100, 1024])
+def test_layernorm_row_mask_zeroes_padded_rows(cols):
+    """Final-norm semantics of a padded row (src/torch_transformer_benchmark.py:170-171)."""
+    rows = 37
+    x = seeded(rows, cols, seed=cols) * 3
+    w, b = seeded(cols, seed=cols + 1) + 1.0, seeded(cols, seed=cols + 2)
+    valid = torch.rand(rows, generator=torch.Generator().manual_seed(cols)) < 0.5
+    ref = ob.layer_norm_ref(x, w, b, 1e-5).masked_fill(~valid[:, None], 0)
+    y = ops.ln_fwd(x.to(DEV), w.to(DEV), b.to(DEV), 1e-5, torch.float32, row_valid=valid.to(DEV))
+    torch.testing.assert_close(y.cpu(), ref, atol=1e-5, rtol=1e-5)
+    assert bool((y.cpu()[~valid] == 0).all())
+
+
 def test_layernorm_three_dim_and_noncontiguous():
     x = seeded(3, 5, 128, seed=21)
     r = seeded(3, 5, 128, dtype=torch.float16, seed=22)
@@ -159,6 +172,43 @@ def test_gemm_residual_inplace(m, n, k):
     assert out.data_ptr() == rg.data_ptr()
     # fp32 output: accumulation-order differences only
     torch.testing.assert_close(out.cpu(), resid + ref, atol=5e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("mode", ["keep", "zero"])
+def test_gemm_residual_row_mask(mode):
+    """Padded rows of the residual update: the product counts as 0 (keep resid,
+    after attention) or the row becomes 0 (after the FFN)."""
+    m, n, k = 300, 192, 64
+    a, w, bias, ref = _gemm_inputs(m, n, k, seed=12)
+    resid = seeded(m, n, seed=13)
+    valid = torch.rand(m, generator=torch.Generator().manual_seed(14)) < 0.6
+    a[~valid] = float("nan")  # a padded row's input may be non-finite (fully masked attention row)
+    code = ops.TK_ROWS_KEEP_RESID if mode == "keep" else ops.TK_ROWS_ZERO
+    out = ops.linear_residual(a.to(DEV), w.to(DEV), bias.to(DEV), resid.to(DEV), row_valid=valid.to(DEV),
+                              row_mode=code).cpu()
+    want = torch.where(valid[:, None], resid + ref, resid if mode == "keep" else torch.zeros_like(resid))
+    torch.testing.assert_close(out[valid], want[valid], atol=5e-5, rtol=1e-5)
+    assert torch.equal(out[~valid], want[~valid])
+
+
+@pytest.mark.parametrize("mode", ["keep", "zero", "zero_all"])
+def test_gemm_add_layernorm_row_mask(mode):
+    m, n, k = 200, 128, 256
+    a, w, bias, acc = _gemm_inputs(m, n, k, seed=15)
+    resid = seeded(m, n, seed=16) * 2
+    lw, lb = seeded(n, seed=17) * 0.3 + 1, seeded(n, seed=18) * 0.3
+    valid = torch.rand(m, generator=torch.Generator().manual_seed(19)) < 0.5
+    a[~valid] = float("nan")
+    code = {"keep": ops.TK_ROWS_KEEP_RESID, "zero": ops.TK_ROWS_ZERO, "zero_all": ops.TK_ROWS_ZERO_ALL}[mode]
+    s_ref = torch.where(valid[:, None], resid + acc, resid if mode == "keep" else torch.zeros_like(resid))
+    h_ref = ob.layer_norm_ref(s_ref, lw, lb, 1e-5)
+    if mode == "zero_all":
+        h_ref = h_ref.masked_fill(~valid[:, None], 0)
+    sg = torch.empty(m, n, device=DEV)
+    h = ops.linear_add_ln(a.to(DEV), w.to(DEV), bias.to(DEV), resid.to(DEV), lw.to(DEV), lb.to(DEV), 1e-5,
+                          torch.float32, sum_out=sg, row_valid=valid.to(DEV), row_mode=code)
+    torch.testing.assert_close(sg.cpu(), s_ref, atol=5e-5, rtol=1e-5)
+    torch.testing.assert_close(h.cpu(), h_ref, atol=1e-4, rtol=1e-4)
 
 
 def test_gemm_strided_operand():
@@ -291,6 +341,34 @@ def test_flash_attention_large_logits(hd):
         out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
         bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
         assert bad == 0, (causal, err)
+
+
+def _attention_ref_keymask(q, k, v, scale, causal, key_valid):
+    """Baseline order (src/torch_transformer_benchmark.py:97-112) with the key mask of :105-108."""
+    scores = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale
+    probs = ob.masked_softmax_ref(scores, causal, key_valid[:, None, None, :])
+    b, h, s, hd = q.shape
+    return torch.matmul(probs, v.float()).transpose(1, 2).reshape(b, s, h * hd)
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 128, 32), (3, 2, 100, 64), (2, 2, 700, 128), (1, 2, 64, 16)],
+                         ids=lambda s: "b{}h{}s{}d{}".format(*s))
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_flash_attention_key_mask(shape, causal):
+    """Per-batch key validity (prefix and holes); rows with at least one valid key
+    match the masked baseline, rows with none come out non-finite as the baseline's."""
+    b, h, s, hd = shape
+    q, k, v = _qkv(shape, seed=31)
+    g = torch.Generator().manual_seed(s)
+    kv = torch.rand(b, s, generator=g) < 0.7
+    kv[0, s // 2:] = False  # a prefix mask in batch 0
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal, key_valid=kv.to(DEV)).cpu()
+    ref = _attention_ref_keymask(q, k, v, hd ** -0.5, causal, kv)
+    allowed = torch.ones(s, s, dtype=torch.bool).tril() if causal else torch.ones(s, s, dtype=torch.bool)
+    seen = (kv[:, None, :] & allowed[None]).any(-1)  # [b, s]: query rows with a valid key
+    bad, err = or_rule_violations(out[seen], ref[seen])
+    assert bad == 0, err
+    assert not bool(torch.isfinite(out[~seen]).all()) or not bool((~seen).any())
 
 
 def test_attention_support_probes():

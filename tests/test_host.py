@@ -133,13 +133,18 @@ def test_capability_probes():
 @pytest.mark.parametrize(
     "fn,args,code",
     [
-        ("tk_ln_cast", (None, None, None, None, 1, 4, 64, 1e-5, None), _lib.TK_ERR_ARG),
-        ("tk_ln_cast", (8, 8, 8, 8, 1, 4, 9000, 1e-5, None), _lib.TK_ERR_ARG),
-        ("tk_ln_cast", (8, 8, 8, 8, 7, 4, 64, 1e-5, None), _lib.TK_ERR_ARG),
-        ("tk_gemm", (16, 12, 16, 12, None, None, 0, 16, 16, 4, 4, 12, 0, None), _lib.TK_ERR_ARG),
-        ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 9, None), _lib.TK_ERR_ARG),
-        ("tk_gemm_bias_add_ln", (16, 16, 16, 16, None, 16, 16, 16, None, 16, 1, 4, 384, 16, 1e-5, None),
+        ("tk_ln_cast", (None, None, None, None, 1, 4, 64, 1e-5, None, None), _lib.TK_ERR_ARG),
+        ("tk_ln_cast", (8, 8, 8, 8, 1, 4, 9000, 1e-5, None, None), _lib.TK_ERR_ARG),
+        ("tk_ln_cast", (8, 8, 8, 8, 7, 4, 64, 1e-5, None, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 12, 16, 12, None, None, 0, 16, 16, 4, 4, 12, 0, None, 0, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 9, None, 0, None), _lib.TK_ERR_ARG),
+        # a row mask needs the residual epilogue and a valid tk_row_mode
+        ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 0, 16, 1, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 16, 16, 16, None, 16, 16, 16, 16, 4, 4, 16, 2, 16, 7, None), _lib.TK_ERR_ARG),
+        ("tk_gemm_bias_add_ln", (16, 16, 16, 16, None, 16, 16, 16, None, 16, 1, 4, 384, 16, 1e-5, None, 0, None),
          _lib.TK_ERR_UNSUPPORTED),
+        ("tk_gemm_bias_add_ln", (16, 16, 16, 16, None, 16, 16, 16, None, 16, 1, 4, 128, 16, 1e-5, 16, 0, None),
+         _lib.TK_ERR_ARG),
         ("tk_masked_softmax", (None, None, 1, 4, 1, None, 1, None), _lib.TK_ERR_ARG),
     ],
 )
@@ -153,6 +158,14 @@ def test_argument_validation_without_gpu(fn, args, code):
 def test_flash_rejects_bad_head_dim_without_gpu():
     lib = _lib.load()
     st = _lib.strides3((0, 0, 0))
-    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 48, st, st, st, st, 1.0, 1, None)
+    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 48, st, st, st, st, 1.0, 1, None, 0, None)
     assert status == _lib.TK_ERR_UNSUPPORTED
     assert "head_dim" in lib.tk_last_error_string().decode()
+
+
+def test_flash_rejects_short_key_mask_stride_without_gpu():
+    lib = _lib.load()
+    st = _lib.strides3((64, 64, 64))
+    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 2, 1, 8, 64, st, st, st, st, 1.0, 1, 16, 4, None)
+    assert status == _lib.TK_ERR_ARG
+    assert "key_valid_stride" in lib.tk_last_error_string().decode()

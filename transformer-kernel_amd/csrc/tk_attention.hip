@@ -75,6 +75,8 @@ struct AttnArgs {
   const f16* v;
   f16* o;
   int64_t qs[3], ks[3], vs[3], os[3];  // element strides for (b, h, s)
+  const uint8_t* kv;                   // nullable key validity, [b * kvs + key]
+  int64_t kvs;
   int B, H, S;
   float scale_log2;  // scale * log2(e)
 };
@@ -82,7 +84,9 @@ struct AttnArgs {
 // The body is a __device__ function (the __global__ wrapper below only calls
 // it): device-only builtins used directly in a kernel template's lambdas
 // would make the host-side instantiation, and with it the launch stub, fail.
-template <int HD, int NW, bool CAUSAL>
+// KMASK: the key-validity mask p.kv is applied (a separate instantiation, so
+// the unmasked kernels carry none of its registers or loads).
+template <int HD, int NW, bool CAUSAL, bool KMASK>
 __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
   constexpr int BM = 32 * NW;
   constexpr int NT = NW * 64;
@@ -119,6 +123,7 @@ __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
   const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
   const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
   const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kvs : nullptr;
 
   const int my_row = q0 + wave * 32 + (lane & 31);
   const int g = lane >> 5;
@@ -224,18 +229,24 @@ __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
 
   // ---- softmax of one tile's scores + O^T += V^T . P^T ----
   // accumulator entry r of block kb2 is key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4
-  auto softmax_pv = [&](int kt, int stage, f32x16 (&sacc)[2]) {
+  // kbyte: this lane's byte of the tile's key-validity mask (key k0 + lane),
+  // loaded one step ahead; the wave ballot turns it into one 64-bit word.
+  auto softmax_pv = [&](int kt, int stage, f32x16 (&sacc)[2], int kbyte) {
     const int k0 = kt * kBN;
     const char* vs_ = smem + stage * STAGE + KSTAGE;
-    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min);
+    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
     float mx = -INFINITY;
     if (need_mask) {
+      // bit j of kbits: key k0 + 4*g + j is valid
+      const uint64_t kbits = KMASK ? (uint64_t)__ballot(kbyte != 0) >> (4 * g) : 0ull;
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kb2 * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= p.S || (CAUSAL && key > my_row)) sacc[kb2][r] = -INFINITY;
+          const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+          const int key = k0 + j + 4 * g;
+          if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kbits >> j) & 1) == 0))
+            sacc[kb2][r] = -INFINITY;
           mx = fmaxf(mx, sacc[kb2][r]);
         }
     } else {
@@ -307,17 +318,21 @@ __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
   if (needs(0)) scores(0, s_a);
 
   // One step: prefetch tile kt+2, scores of kt+1 (into s_next), softmax+PV of kt.
+  auto key_byte = [&](int kt) { return KMASK ? (int)kvb[min(kt * kBN + lane, p.S - 1)] : 1; };
+  int kbyte_cur = key_byte(0);
   auto step = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_next)[2]) {
     const int st_cur = kt % kStages;
     const int st_nxt = (kt + 1) % kStages;
     const int st_pre = (kt + 2) % kStages;
     const bool pre = kt + 2 < n_kt;
+    const int kbyte = kbyte_cur;
+    if (kt + 1 < n_kt) kbyte_cur = key_byte(kt + 1);
     if (pre) {
       load_k(kt + 2, st_pre);
       load_v(kt + 2);
     }
     if (kt + 1 < n_kt && needs(kt + 1)) scores(st_nxt, s_next);
-    if (needs(kt)) softmax_pv(kt, st_cur, s_cur);
+    if (needs(kt)) softmax_pv(kt, st_cur, s_cur, kbyte);
     if (pre) {
       __builtin_amdgcn_s_waitcnt(0);
       store_v(st_pre);
@@ -348,9 +363,9 @@ __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
   }
 }
 
-template <int HD, int NW, bool CAUSAL>
+template <int HD, int NW, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(AttnArgs p) {
-  flash_fwd_body<HD, NW, CAUSAL>(p);
+  flash_fwd_body<HD, NW, CAUSAL, KMASK>(p);
 }
 
 template <int HD, int NW>
@@ -358,10 +373,16 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   constexpr int BM = 32 * NW;
   const int64_t n_qt = (p.S + BM - 1) / BM;
   const int64_t grid = n_qt * p.B * p.H;
-  if (causal)
-    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, true>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
+  const dim3 g((unsigned)grid), blk(NW * 64);
+  const bool km = p.kv != nullptr;
+  if (causal && km)
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, true, true>), g, blk, 0, st, p);
+  else if (causal)
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, true, false>), g, blk, 0, st, p);
+  else if (km)
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, false, true>), g, blk, 0, st, p);
   else
-    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, false>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((flash_fwd_kernel<HD, NW, false, false>), g, blk, 0, st, p);
   return check_launch("tk_flash_attn_fwd");
 }
 
@@ -387,7 +408,8 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
                                  int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
                                  const int64_t* q_strides, const int64_t* k_strides,
                                  const int64_t* v_strides, const int64_t* o_strides, float scale,
-                                 int causal, void* stream) {
+                                 int causal, const uint8_t* key_valid, int64_t key_valid_stride,
+                                 void* stream) {
   TK_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && o_strides, TK_ERR_ARG,
              "tk_flash_attn_fwd: null pointer");
   TK_REQUIRE(tk_attention_supported(head_dim), TK_ERR_UNSUPPORTED,
@@ -412,6 +434,10 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
   for (int i = 0; i < 3; ++i) {
     p.qs[i] = q_strides[i]; p.ks[i] = k_strides[i]; p.vs[i] = v_strides[i]; p.os[i] = o_strides[i];
   }
+  TK_REQUIRE(key_valid == nullptr || key_valid_stride >= seq, TK_ERR_ARG,
+             "tk_flash_attn_fwd: key_valid_stride=%lld < seq=%lld", (long long)key_valid_stride, (long long)seq);
+  p.kv = key_valid;
+  p.kvs = key_valid_stride;
   p.B = (int)batch; p.H = (int)heads; p.S = (int)seq;
   p.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);

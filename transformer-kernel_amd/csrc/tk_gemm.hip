@@ -37,6 +37,8 @@ struct GemmArgs {
   const float* ln_w;
   const float* ln_b;
   float* sum_out;
+  const uint8_t* row_valid;  // nullable: padded rows (tk_row_mode)
+  int row_mode;
   int64_t lda, ldw, ldr, ldc;
   int M, N, K;
   float eps;
@@ -438,6 +440,9 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
           const f32x4 d = *reinterpret_cast<const f32x4*>(src);
           const float* rr = p.resid + (int64_t)m * p.ldr + n;
           float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
+          // padded row: the product counts as 0 (keep resid) or the row is 0
+          const bool valid = p.row_valid == nullptr || p.row_valid[m] != 0;
+          const bool keep = p.row_mode == TK_ROWS_KEEP_RESID;
           if (p.vec && n + 3 < p.N) {
             const f32x4 r = *reinterpret_cast<const f32x4*>(rr);
             f32x4 b = {0.f, 0.f, 0.f, 0.f};
@@ -445,11 +450,13 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
               if (p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
               else b = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
             }
-            *reinterpret_cast<f32x4*>(cr) = f32x4{r[0] + (d[0] + b[0]), r[1] + (d[1] + b[1]),
-                                                  r[2] + (d[2] + b[2]), r[3] + (d[3] + b[3])};
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = valid ? r[e] + (d[e] + b[e]) : (keep ? r[e] : 0.f);
+            *reinterpret_cast<f32x4*>(cr) = o;
           } else {
             for (int e = 0; e < 4 && n + e < p.N; ++e)
-              cr[e] = rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f));
+              cr[e] = valid ? rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f)) : (keep ? rr[e] : 0.f);
           }
         } else {
           const f16x8 d = *reinterpret_cast<const f16x8*>(src);
@@ -506,7 +513,15 @@ __global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
   const int ml = wm * ML::WM + (lane & 31);  // tile-local row of fragment j=0
   const int n_w = wn * ML::WN + 4 * (lane >> 5);
 
-  // s = resid + acc + bias, kept in acc.
+  // s = resid + acc + bias, kept in acc.  A padded row (row_valid) takes
+  // s = resid (TK_ROWS_KEEP_RESID) or s = 0.
+  bool valid[ML::FM];
+#pragma unroll
+  for (int j = 0; j < ML::FM; ++j) {
+    const int m = m0 + ml + j * 32;
+    valid[j] = p.row_valid == nullptr || (m < p.M && p.row_valid[m] != 0);
+  }
+  const bool keep = p.row_mode == TK_ROWS_KEEP_RESID;
 #pragma unroll
   for (int i = 0; i < ML::FN; ++i)
 #pragma unroll
@@ -519,7 +534,8 @@ __global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
         f32x4 r = {0, 0, 0, 0};
         if (m < p.M) r = *reinterpret_cast<const f32x4*>(p.resid + (int64_t)m * p.ldr + n);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += bv[e] + r[e];
+        for (int e = 0; e < 4; ++e)
+          acc[i][j][4 * q + e] = valid[j] ? acc[i][j][4 * q + e] + (bv[e] + r[e]) : (keep ? r[e] : 0.f);
       }
     }
 
@@ -578,10 +594,11 @@ __global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
         const int m = m0 + ml + j * 32;
         if (m >= p.M) continue;
         float s[4], h[4];
+        const bool zero_h = !valid[j] && p.row_mode == TK_ROWS_ZERO_ALL;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           s[e] = acc[i][j][4 * q + e];
-          h[e] = (s[e] - mean[j]) * rstd[j] * gw[e] + gb[e];
+          h[e] = zero_h ? 0.f : (s[e] - mean[j]) * rstd[j] * gw[e] + gb[e];
         }
         if (p.sum_out)
           *reinterpret_cast<f32x4*>(p.sum_out + (int64_t)m * p.N + n) = f32x4{s[0], s[1], s[2], s[3]};
@@ -650,7 +667,8 @@ using namespace tk;
 
 extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t ldw,
                        const float* bias, const float* resid, int64_t ldr, void* c, int64_t ldc,
-                       int64_t m, int64_t n, int64_t k, int epilogue, void* stream) {
+                       int64_t m, int64_t n, int64_t k, int epilogue, const uint8_t* row_valid,
+                       int row_mode, void* stream) {
   TK_REQUIRE(a && w && c, TK_ERR_ARG, "tk_gemm: null pointer");
   TK_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
              TK_ERR_ARG, "tk_gemm: bad sizes m=%lld n=%lld k=%lld", (long long)m, (long long)n,
@@ -664,8 +682,13 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
   TK_REQUIRE(ldc >= n, TK_ERR_ARG, "tk_gemm: ldc=%lld < n=%lld", (long long)ldc, (long long)n);
   if (epilogue == TK_EPI_BIAS_RESID)
     TK_REQUIRE(resid != nullptr && ldr >= n, TK_ERR_ARG, "tk_gemm: residual epilogue needs resid, ldr >= n");
+  TK_REQUIRE(row_valid == nullptr || (epilogue == TK_EPI_BIAS_RESID && row_mode >= TK_ROWS_KEEP_RESID &&
+                                      row_mode <= TK_ROWS_ZERO_ALL),
+             TK_ERR_ARG, "tk_gemm: row_valid needs the residual epilogue and a tk_row_mode (got %d)", row_mode);
   if (m == 0 || n == 0) return TK_OK;
   GemmArgs p{};
+  p.row_valid = row_valid;
+  p.row_mode = row_mode;
   // 16-byte vector stores (and residual loads) when every output row start
   // is aligned for them; element-wise otherwise.
   if (epilogue == TK_EPI_BIAS_RESID)
@@ -693,7 +716,8 @@ extern "C" int tk_gemm_ln_supported(int64_t n) { return n == 128 || n == 256 || 
 extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half* w, int64_t ldw,
                                    const float* bias, const float* resid, const float* ln_w,
                                    const float* ln_b, float* sum_out, void* h_out, int h_dtype,
-                                   int64_t m, int64_t n, int64_t k, float eps, void* stream) {
+                                   int64_t m, int64_t n, int64_t k, float eps, const uint8_t* row_valid,
+                                   int row_mode, void* stream) {
   TK_REQUIRE(a && w && resid && ln_w && ln_b && h_out, TK_ERR_ARG, "tk_gemm_bias_add_ln: null pointer");
   TK_REQUIRE(tk_gemm_ln_supported(n), TK_ERR_UNSUPPORTED,
              "tk_gemm_bias_add_ln: row width n=%lld not in {128, 256, 512}", (long long)n);
@@ -706,8 +730,12 @@ extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half*
                  aligned16(h_out) && (sum_out == nullptr || aligned16(sum_out)) &&
                  (bias == nullptr || aligned16(bias)),
              TK_ERR_ARG, "tk_gemm_bias_add_ln: buffers must be 16-byte aligned");
+  TK_REQUIRE(row_valid == nullptr || (row_mode >= TK_ROWS_KEEP_RESID && row_mode <= TK_ROWS_ZERO_ALL),
+             TK_ERR_ARG, "tk_gemm_bias_add_ln: bad row_mode %d", row_mode);
   if (m == 0) return TK_OK;
   GemmArgs p{};
+  p.row_valid = row_valid;
+  p.row_mode = row_mode;
   p.a = reinterpret_cast<const f16*>(a);
   p.w = reinterpret_cast<const f16*>(w);
   p.bias = bias;

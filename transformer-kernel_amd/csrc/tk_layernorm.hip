@@ -44,12 +44,13 @@ struct Vec<f16> {
   static __device__ __forceinline__ void store1(f16* p, float v) { *p = (f16)v; }
 };
 
-// HAS_Y: s = x + y (residual add) else s = x.
+// HAS_Y: s = x + y (residual add) else s = x.  row_valid (nullable): an
+// invalid row's normalised output is written as zeros.
 template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT>
 __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
     const float* x, const YT* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ b, float* sum_out, OT* __restrict__ out, int64_t rows,
-    int cols, float eps) {
+    int cols, float eps, const uint8_t* __restrict__ row_valid) {
   constexpr int kRowsPerBlock = kBlock / LPR;
   const int lane = threadIdx.x % LPR;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
@@ -113,7 +114,10 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
     }
   }
   const float var = group_sum<LPR>(acc) / (float)cols;
-  const float rstd = 1.0f / sqrtf(var + eps);
+  float rstd = 1.0f / sqrtf(var + eps);
+  // padded row: (s - mean) * 0 * w + 0 written as exact zeros
+  const bool keep = row_valid == nullptr || row_valid[row] != 0;
+  if (!keep) rstd = 0.f;
 
   OT* orow = out + row * cols;
 #pragma unroll
@@ -125,10 +129,10 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
         const f32x4 bv = *reinterpret_cast<const f32x4*>(b + c0);
         float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = s[v * 4 + e] * rstd * wv[e] + bv[e];
+        for (int e = 0; e < 4; ++e) o[e] = keep ? s[v * 4 + e] * rstd * wv[e] + bv[e] : 0.f;
         Vec<OT>::store4(orow + c0, o);
       } else {
-        Vec<OT>::store1(orow + c0, s[v] * rstd * w[c0] + b[c0]);
+        Vec<OT>::store1(orow + c0, keep ? s[v] * rstd * w[c0] + b[c0] : 0.f);
       }
     }
   }
@@ -136,20 +140,20 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
 
 template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT>
 int launch_rows(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
-                OT* out, int64_t rows, int cols, float eps, hipStream_t st) {
+                OT* out, int64_t rows, int cols, float eps, const uint8_t* row_valid, hipStream_t st) {
   constexpr int kRowsPerBlock = kBlock / LPR;
   const int64_t grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, YT, OT>), dim3((unsigned)grid),
-                     dim3(kBlock), 0, st, x, y, w, b, sum_out, out, rows, cols, eps);
+                     dim3(kBlock), 0, st, x, y, w, b, sum_out, out, rows, cols, eps, row_valid);
   return check_launch("layernorm");
 }
 
 // Picks lanes-per-row and register-vector count for `cols`.
 template <bool HAS_Y, typename YT, typename OT>
 int dispatch(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
-             OT* out, int64_t rows, int cols, float eps, hipStream_t st) {
+             OT* out, int64_t rows, int cols, float eps, const uint8_t* row_valid, hipStream_t st) {
 #define TK_LN(LPR, NV, VW) \
-  return launch_rows<LPR, NV, VW, HAS_Y, YT, OT>(x, y, w, b, sum_out, out, rows, cols, eps, st)
+  return launch_rows<LPR, NV, VW, HAS_Y, YT, OT>(x, y, w, b, sum_out, out, rows, cols, eps, row_valid, st)
   // 16-byte vector path needs cols % 4 == 0 and 16-byte aligned fp32 rows
   // (8-byte for fp16 rows); anything else takes the scalar path.
   auto al = [](const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; };
@@ -188,7 +192,8 @@ constexpr int64_t kMaxCols = 8192;
 using namespace tk;
 
 extern "C" int tk_ln_cast(const float* x, const float* w, const float* b, void* out,
-                          int out_dtype, int64_t rows, int64_t cols, float eps, void* stream) {
+                          int out_dtype, int64_t rows, int64_t cols, float eps,
+                          const uint8_t* row_valid, void* stream) {
   TK_REQUIRE(x && w && b && out, TK_ERR_ARG, "tk_ln_cast: null pointer");
   TK_REQUIRE(rows >= 0 && cols >= 1 && cols <= kMaxCols, TK_ERR_ARG,
              "tk_ln_cast: rows=%lld cols=%lld outside [0, inf) x [1, %lld]", (long long)rows,
@@ -199,8 +204,8 @@ extern "C" int tk_ln_cast(const float* x, const float* w, const float* b, void* 
   hipStream_t st = as_stream(stream);
   const int c = (int)cols;
   if (out_dtype == TK_F16)
-    return dispatch<false, float, f16>(x, nullptr, w, b, nullptr, (f16*)out, rows, c, eps, st);
-  return dispatch<false, float, float>(x, nullptr, w, b, nullptr, (float*)out, rows, c, eps, st);
+    return dispatch<false, float, f16>(x, nullptr, w, b, nullptr, (f16*)out, rows, c, eps, row_valid, st);
+  return dispatch<false, float, float>(x, nullptr, w, b, nullptr, (float*)out, rows, c, eps, row_valid, st);
 }
 
 extern "C" int tk_add_ln_cast(const float* x, const void* y, int y_dtype, const float* w,
@@ -217,10 +222,11 @@ extern "C" int tk_add_ln_cast(const float* x, const void* y, int y_dtype, const 
   const int c = (int)cols;
   if (y_dtype == TK_F16) {
     if (h_dtype == TK_F16)
-      return dispatch<true, f16, f16>(x, (const f16*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, st);
-    return dispatch<true, f16, float>(x, (const f16*)y, w, b, sum_out, (float*)h_out, rows, c, eps, st);
+      return dispatch<true, f16, f16>(x, (const f16*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr, st);
+    return dispatch<true, f16, float>(x, (const f16*)y, w, b, sum_out, (float*)h_out, rows, c, eps, nullptr, st);
   }
   if (h_dtype == TK_F16)
-    return dispatch<true, float, f16>(x, (const float*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, st);
-  return dispatch<true, float, float>(x, (const float*)y, w, b, sum_out, (float*)h_out, rows, c, eps, st);
+    return dispatch<true, float, f16>(x, (const float*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr, st);
+  return dispatch<true, float, float>(x, (const float*)y, w, b, sum_out, (float*)h_out, rows, c, eps, nullptr,
+                                      st);
 }

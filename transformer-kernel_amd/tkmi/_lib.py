@@ -13,11 +13,12 @@ import threading
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_void_p
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtkmi.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TK_OK, TK_ERR_ARG, TK_ERR_UNSUPPORTED, TK_ERR_HIP = 0, -1, -2, -3
 TK_F32, TK_F16 = 0, 1
 TK_EPI_BIAS, TK_EPI_BIAS_GELU, TK_EPI_BIAS_RESID = 0, 1, 2
+TK_ROWS_KEEP_RESID, TK_ROWS_ZERO, TK_ROWS_ZERO_ALL = 1, 2, 3
 
 _I64_3 = c_int64 * 3
 
@@ -25,7 +26,9 @@ _I64_3 = c_int64 * 3
 SIGNATURES = {
     "tk_version": (c_int, []),
     "tk_last_error_string": (ctypes.c_char_p, []),
-    "tk_ln_cast": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float, c_void_p]),
+    "tk_ln_cast": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float, c_void_p, c_void_p]
+    ),
     "tk_add_ln_cast": (
         c_int,
         [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float, c_void_p],
@@ -33,18 +36,19 @@ SIGNATURES = {
     "tk_gemm": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
-         c_int64, c_int64, c_int64, c_int, c_void_p],
+         c_int64, c_int64, c_int64, c_int, c_void_p, c_int, c_void_p],
     ),
     "tk_gemm_bias_add_ln": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_int, c_int64, c_int64, c_int64, c_float, c_void_p],
+         c_void_p, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int, c_void_p],
     ),
     "tk_gemm_ln_supported": (c_int, [c_int64]),
     "tk_flash_attn_fwd": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-         POINTER(c_int64), POINTER(c_int64), POINTER(c_int64), POINTER(c_int64), c_float, c_int, c_void_p],
+         POINTER(c_int64), POINTER(c_int64), POINTER(c_int64), POINTER(c_int64), c_float, c_int,
+         c_void_p, c_int64, c_void_p],
     ),
     "tk_attention_supported": (c_int, [c_int64]),
     "tk_masked_softmax": (

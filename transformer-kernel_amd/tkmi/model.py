@@ -181,17 +181,23 @@ class OptimizedTransformer(BaselineTransformer):
             )
         if x.dim() != 3 or x.shape[-1] != self.d_model:
             raise ValueError(f"expected [B, S, {self.d_model}] input, got {tuple(x.shape)}")
+        mask = None
         if not self._mask_is_dense(valid_token_mask):
-            raise NotImplementedError(
-                "padded valid_token_mask is not supported by the MI355X kernels yet "
-                "(dense masks only)"
-            )
+            if tuple(valid_token_mask.shape) != tuple(x.shape[:2]):
+                raise ValueError(f"valid_token_mask must be [B, S] = {tuple(x.shape[:2])}, "
+                                 f"got {tuple(valid_token_mask.shape)}")
+            mask = valid_token_mask.to(device=x.device, dtype=torch.bool).contiguous()
         if not ops.attention_supported(self.head_dim, torch.float16, x.device):
             raise NotImplementedError(f"head_dim {self.head_dim} is not supported by the attention kernel")
-        out = self._run_layers(x)
+        out = self._run_layers(x, mask)
         return out.to(x.dtype)
 
-    def _run_layers(self, x: torch.Tensor) -> torch.Tensor:
+    def _run_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The fused schedule; ``mask`` ([B, S] bool, None when dense) follows the
+        baseline's padding semantics (src/torch_transformer_benchmark.py:105-121,
+        143-144,170-171): padded keys are masked in attention, a padded row's
+        attention output is 0 (the residual keeps x), its block output is 0,
+        and its final-norm output is 0."""
         bsz, seq, d = x.shape
         t = bsz * seq
         nh, hd = self.num_heads, self.head_dim
@@ -212,6 +218,7 @@ class OptimizedTransformer(BaselineTransformer):
         fuse = (self.settings.fused_norm and d <= self.settings.fused_norm_max_d
                 and ops.gemm_ln_supported(d))
 
+        rows = mask.view(t) if mask is not None else None
         ops.ln_fwd(xin, weights[0].n1_w, weights[0].n1_b, weights[0].n1_eps, torch.float16, out=h,
                    name="ln_in")
         src = xin  # residual stream input of the next add (the caller's x is never written)
@@ -221,12 +228,14 @@ class OptimizedTransformer(BaselineTransformer):
         last = len(weights) - 1
         for i, lw in enumerate(weights):
             ops.linear(h, lw.w_qkv, lw.b_qkv, out=qkv, name="qkv")
-            ops.flash_attention(q, k, v, self.attn_scale, self.config.causal, out=ctx3)
+            ops.flash_attention(q, k, v, self.attn_scale, self.config.causal, out=ctx3, key_valid=mask)
             if fuse:
                 ops.linear_add_ln(ctx, lw.w_o, lw.b_o, src, lw.n2_w, lw.n2_b, lw.n2_eps,
-                                  sum_out=resid, h_out=h, name="out_proj_ln")
+                                  sum_out=resid, h_out=h, name="out_proj_ln",
+                                  row_valid=rows, row_mode=ops.TK_ROWS_KEEP_RESID)
             else:
-                ops.linear_residual(ctx, lw.w_o, lw.b_o, src, out=resid, name="out_proj_resid")
+                ops.linear_residual(ctx, lw.w_o, lw.b_o, src, out=resid, name="out_proj_resid",
+                                    row_valid=rows, row_mode=ops.TK_ROWS_KEEP_RESID)
                 ops.ln_fwd(resid, lw.n2_w, lw.n2_b, lw.n2_eps, torch.float16, out=h, name="ln2")
             src = resid
             ops.linear(h, lw.w_1, lw.b_1, gelu=True, out=u, name="ffn_up_gelu")
@@ -238,9 +247,13 @@ class OptimizedTransformer(BaselineTransformer):
                 dst, keep_sum = out, False  # final norm: the summed residual is dead
             if fuse:
                 ops.linear_add_ln(u, lw.w_2, lw.b_2, resid, nw, nb, neps,
-                                  sum_out=resid if keep_sum else None, h_out=dst, name="ffn_down_ln")
+                                  sum_out=resid if keep_sum else None, h_out=dst, name="ffn_down_ln",
+                                  row_valid=rows,
+                                  row_mode=ops.TK_ROWS_ZERO if keep_sum else ops.TK_ROWS_ZERO_ALL)
             else:
-                ops.linear_residual(u, lw.w_2, lw.b_2, resid, out=resid, name="ffn_down_resid")
+                ops.linear_residual(u, lw.w_2, lw.b_2, resid, out=resid, name="ffn_down_resid",
+                                    row_valid=rows, row_mode=ops.TK_ROWS_ZERO)
                 ops.ln_fwd(resid, nw, nb, neps, dst.dtype, out=dst,
-                           name="ln_next" if keep_sum else "ln_final")
+                           name="ln_next" if keep_sum else "ln_final",
+                           row_valid=None if keep_sum else rows)
         return out.view(bsz, seq, d)

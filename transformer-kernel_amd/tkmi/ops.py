@@ -20,7 +20,8 @@ from typing import List, Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import TK_EPI_BIAS, TK_EPI_BIAS_GELU, TK_EPI_BIAS_RESID, TK_F16, TK_F32
+from ._lib import (TK_EPI_BIAS, TK_EPI_BIAS_GELU, TK_EPI_BIAS_RESID, TK_F16, TK_F32, TK_ROWS_KEEP_RESID,
+                   TK_ROWS_ZERO, TK_ROWS_ZERO_ALL)
 
 MAX_FUSED_SIZE = 8192  # longest LayerNorm row (src/fused_kernels.py:59)
 
@@ -87,9 +88,23 @@ def can_fuse(x: torch.Tensor) -> bool:
     return x.is_cuda and x.shape[-1] <= MAX_FUSED_SIZE and _lib.is_available()
 
 
+def _row_mask(mask, rows: int):
+    """A [rows] byte view of a bool / uint8 validity mask (nonzero = valid), or None."""
+    if mask is None:
+        return None
+    if mask.numel() != rows or mask.dtype not in (torch.bool, torch.uint8):
+        raise ValueError(f"row mask must be bool/uint8 with {rows} elements, got {mask.dtype} {tuple(mask.shape)}")
+    _require_cuda(mask)
+    return mask.reshape(rows).contiguous()
+
+
 def ln_fwd(x, weight, bias, eps: float, out_dtype: Optional[torch.dtype] = None, out=None,
-           name: str = "ln_cast"):
-    """LayerNorm over the last dim, fp32 statistics, output in ``out_dtype``."""
+           name: str = "ln_cast", row_valid=None):
+    """LayerNorm over the last dim, fp32 statistics, output in ``out_dtype``.
+
+    ``row_valid`` (optional bool mask over the rows): invalid rows are written
+    as zeros (the masked final norm, src/torch_transformer_benchmark.py:170-171).
+    """
     _require_cuda(x, weight, bias)
     out_dtype = x.dtype if out_dtype is None else out_dtype
     shape = x.shape
@@ -99,9 +114,10 @@ def ln_fwd(x, weight, bias, eps: float, out_dtype: Optional[torch.dtype] = None,
     b = bias.float().contiguous()
     if out is None:
         out = torch.empty(x2.shape, dtype=out_dtype, device=x.device)
+    rv = _row_mask(row_valid, x2.shape[0])
     _launch(
         name, "tk_ln_cast", x2.data_ptr(), w.data_ptr(), b.data_ptr(), out.data_ptr(),
-        _code(out_dtype), x2.shape[0], cols, float(eps), _stream(x),
+        _code(out_dtype), x2.shape[0], cols, float(eps), rv.data_ptr() if rv is not None else None, _stream(x),
     )
     return out.view(shape)
 
@@ -158,13 +174,18 @@ def linear(a, w, bias=None, gelu: bool = False, out=None, name: Optional[str] = 
     _launch(
         name or ("gemm_gelu" if gelu else "gemm"), "tk_gemm", a.data_ptr(), a.stride(0), w.data_ptr(),
         w.stride(0), bias.data_ptr() if bias is not None else None, None, 0, out.data_ptr(),
-        out.stride(0), m, n, k, TK_EPI_BIAS_GELU if gelu else TK_EPI_BIAS, _stream(a),
+        out.stride(0), m, n, k, TK_EPI_BIAS_GELU if gelu else TK_EPI_BIAS, None, 0, _stream(a),
     )
     return out
 
 
-def linear_residual(a, w, bias, resid, out=None, name: str = "gemm_resid"):
-    """fp32 ``out = resid + a . w^T + bias``; ``out`` may be ``resid`` (in place)."""
+def linear_residual(a, w, bias, resid, out=None, name: str = "gemm_resid", row_valid=None,
+                    row_mode: int = TK_ROWS_KEEP_RESID):
+    """fp32 ``out = resid + a . w^T + bias``; ``out`` may be ``resid`` (in place).
+
+    ``row_valid`` (optional bool mask over the M rows): an invalid row becomes
+    ``resid`` (``TK_ROWS_KEEP_RESID``) or 0 (``TK_ROWS_ZERO``).
+    """
     _check_gemm_operands(a, w)
     m, k = a.shape
     n = w.shape[0]
@@ -172,10 +193,12 @@ def linear_residual(a, w, bias, resid, out=None, name: str = "gemm_resid"):
         raise ValueError("residual must be fp32 [M, N] with contiguous rows")
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    rv = _row_mask(row_valid, m)
     _launch(
         name, "tk_gemm", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
         bias.data_ptr() if bias is not None else None, resid.data_ptr(), resid.stride(0),
-        out.data_ptr(), out.stride(0), m, n, k, TK_EPI_BIAS_RESID, _stream(a),
+        out.data_ptr(), out.stride(0), m, n, k, TK_EPI_BIAS_RESID, rv.data_ptr() if rv is not None else None,
+        int(row_mode) if rv is not None else 0, _stream(a),
     )
     return out
 
@@ -185,10 +208,14 @@ def gemm_ln_supported(n: int) -> bool:
 
 
 def linear_add_ln(a, w, bias, resid, ln_weight, ln_bias, eps: float, out_dtype=torch.float16,
-                  sum_out=None, h_out=None, name: str = "gemm_add_ln"):
+                  sum_out=None, h_out=None, name: str = "gemm_add_ln", row_valid=None,
+                  row_mode: int = TK_ROWS_KEEP_RESID):
     """``s = resid + a . w^T + bias``; ``h = LN(s)`` in one kernel (full-row tiles).
 
     ``sum_out`` receives s when given (it may be ``resid``); returns h.
+    ``row_valid`` / ``row_mode``: an invalid row takes s = resid
+    (``TK_ROWS_KEEP_RESID``) or s = 0 (``TK_ROWS_ZERO``; ``TK_ROWS_ZERO_ALL``
+    also writes h = 0).
     """
     _check_gemm_operands(a, w)
     m, k = a.shape
@@ -197,11 +224,13 @@ def linear_add_ln(a, w, bias, resid, ln_weight, ln_bias, eps: float, out_dtype=t
         raise ValueError("residual must be contiguous fp32 [M, N]")
     if h_out is None:
         h_out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    rv = _row_mask(row_valid, m)
     _launch(
         name, "tk_gemm_bias_add_ln", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
         bias.data_ptr() if bias is not None else None, resid.data_ptr(), ln_weight.data_ptr(),
         ln_bias.data_ptr(), sum_out.data_ptr() if sum_out is not None else None, h_out.data_ptr(),
-        _code(h_out.dtype), m, n, k, float(eps), _stream(a),
+        _code(h_out.dtype), m, n, k, float(eps), rv.data_ptr() if rv is not None else None,
+        int(row_mode) if rv is not None else 0, _stream(a),
     )
     return h_out
 
@@ -220,12 +249,15 @@ def attention_supported(head_dim: int, dtype: torch.dtype = torch.float16, devic
     return bool(_lib.load().tk_attention_supported(int(head_dim)))
 
 
-def flash_attention(q, k, v, scale: float, causal: bool, out=None):
+def flash_attention(q, k, v, scale: float, causal: bool, out=None, key_valid=None):
     """Exact attention; returns the context as ``[B, S, H*hd]`` fp16.
 
     q/k/v are logically ``[B, H, S, hd]`` fp16 and may be strided views in
     the first three dims (e.g. of the fused ``[B, S, 3, H, hd]`` projection);
-    the last dim must be contiguous.
+    the last dim must be contiguous.  ``key_valid`` (optional ``[B, S]`` bool):
+    invalid keys are masked like future keys
+    (src/torch_transformer_benchmark.py:105-108); a query row with no valid
+    key comes out non-finite, as the baseline's.
     """
     _require_cuda(q, k, v)
     bsz, nh, s, hd = q.shape
@@ -238,11 +270,16 @@ def flash_attention(q, k, v, scale: float, causal: bool, out=None):
     if out is None:
         out = torch.empty((bsz, s, nh * hd), dtype=torch.float16, device=q.device)
     o_strides = (out.stride(0), hd, out.stride(1))
+    kv = None
+    if key_valid is not None:
+        if tuple(key_valid.shape) != (bsz, s):
+            raise ValueError(f"key_valid must be [B, S] = {(bsz, s)}, got {tuple(key_valid.shape)}")
+        kv = _row_mask(key_valid, bsz * s)
     _launch(
         "flash_attn", "tk_flash_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
         bsz, nh, s, hd, _lib.strides3(q.stride()[:3]), _lib.strides3(k.stride()[:3]),
         _lib.strides3(v.stride()[:3]), _lib.strides3(o_strides), float(scale), int(bool(causal)),
-        _stream(q),
+        kv.data_ptr() if kv is not None else None, s, _stream(q),
     )
     return out
 
