@@ -169,3 +169,27 @@ def test_flash_rejects_short_key_mask_stride_without_gpu():
     status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 2, 1, 8, 64, st, st, st, st, 1.0, 1, 16, 4, None)
     assert status == _lib.TK_ERR_ARG
     assert "key_valid_stride" in lib.tk_last_error_string().decode()
+
+
+# Attention instantiations the five benchmark configs dispatch:
+# (head_dim, waves per workgroup, causal) -- C1, C2, C3/C5, C4.
+BENCH_ATTENTION = [(32, 4, 1), (64, 2, 0), (64, 8, 1), (128, 8, 1)]
+
+
+def test_hot_kernels_use_no_scratch():
+    """A spilled accumulator costs several times the kernel's run time and no
+    parity test sees it; the build's resource report must show no scratch for
+    the GEMM, LayerNorm and softmax kernels and the benchmarked attention."""
+    from tkmi import build as tkbuild
+
+    if not tkbuild.RESOURCE_PATH.exists():
+        pytest.skip("library not built")
+    usage = json.loads(tkbuild.RESOURCE_PATH.read_text())
+    hot = [k for k in usage if any(s in k for s in ("gemm_kernel", "gemm_ln_kernel", "ln_rows_kernel", "softmax_"))]
+    assert len(hot) >= 30
+    for hd, nw, causal in BENCH_ATTENTION:
+        hot.append(f"_ZN2tk12_GLOBAL__N_116flash_fwd_kernelILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
+    missing = [k for k in hot if k not in usage]
+    assert not missing, missing
+    spilled = {k: usage[k]["scratch"] for k in hot if usage[k].get("scratch", 0) > 0}
+    assert not spilled, spilled

@@ -1,49 +1,59 @@
 // FlashAttention-2-style forward for gfx950 (fp16 MFMA, fp32 online softmax).
 //
 // Per workgroup: BM = 32*NW query rows of one (batch, head), one wave per 32
-// rows.  Key/value tiles of 64 keys live in three LDS stages; K tiles are
-// copied global -> LDS directly (global_load_lds_dwordx4), V tiles go through
-// registers and are written transposed (V^T).  Tile t+2 is fetched while
-// tile t is consumed.
+// rows, key/value tiles of 64 keys in LDS.
 //
-// Transposed formulation.  Each wave computes S^T = K . Q^T with
-// v_mfma_f32_32x32x16_f16 (A operand = K rows from LDS, B operand = the
-// wave's Q rows, held in registers for the whole kernel).  In the 32x32
-// accumulator layout a lane then holds 16 keys of ONE query row (row =
-// lane & 31; lanes l and l^32 hold the two halves), so
+// Transposed formulation (both kernel bodies).  Each wave computes
+// S^T = K . Q^T with v_mfma_f32_32x32x16_f16 (A operand = K rows from LDS,
+// B operand = the wave's Q rows, held in registers for the whole kernel).
+// In the 32x32 accumulator layout a lane then holds 16 keys of ONE query row
+// (row = lane & 31; lanes l and l^32 hold the two halves), so
 //   * the running max / sum of a row need one lane-pair exchange, no LDS;
 //   * the rescale of the output accumulator is one scalar per lane;
 //   * the fp16 probabilities of 8 consecutive accumulator entries are
-//     directly the B operand of O^T = V^T . P^T.
-// The keys those 8 entries stand for are {16t+8e2+4g+e10}; V^T is stored in
-// LDS with key bits 2 and 3 swapped so that the matching A operand (8 keys
-// of one head-dim row d) is one contiguous 16-byte read.
+//     directly the B operand of O^T = V^T . P^T; those 8 entries stand for
+//     the keys {16t + 8*e2 + 4g + e10} (g = lane >> 5).
 //
-// Software pipeline inside a wave: the S^T MFMAs of tile t+1 are issued
-// before the softmax of tile t, so the exp/max/sum VALU work of one tile runs
-// while the matrix core computes the next tile's scores.
+// Two bodies, picked by head_dim at compile time:
+//   flash_dma_body (head_dim <= 64): K and V tiles copied global -> LDS
+//     directly (global_load_lds_dwordx4, row-major); the V^T operand is two
+//     ds_read_b64_tr_b16 of the row-major V tile.  The O^T MFMAs of tile t-1
+//     are deferred into step t, so every MFMA of a step is independent of
+//     the step's exponentials and interleaves with them; the row max of the
+//     next tile is computed in the same pass.
+//   flash_vreg_body (head_dim 128): the deferred P needs 16 more registers
+//     than two waves per SIMD leave at head_dim 128, so tile t's O^T MFMAs
+//     follow its exponentials; V^T is written to LDS from registers with
+//     key bits 2 and 3 swapped so that each A operand is one 16-byte read.
+//   Measured on MI355X (C5 shape, head_dim 64): the DMA body 5.6-5.8 ms
+//   against 6.2-6.3 ms for the register body; at head_dim 128 (C4 shape)
+//   the register body 1.48 ms against 1.70 ms.
 //
 // Numerics (src/kernels.py:112-134, src/torch_transformer_benchmark.py:97-111):
 // fp32 scores, the scale applied in fp32 after Q.K^T (folded with log2(e)
 // into one FMA before exp2: exp2(s*c - m*c) = exp(scale*(s - m))), -inf
-// masking of future keys, fp32 running max/sum, fp16 P for the PV product,
-// fp32 accumulation, one final divide.
+// masking of future and invalid keys, fp32 running max and sums, fp16 P for
+// the PV product, fp32 accumulation, one final divide.
 #include "tk_common.hpp"
 
 namespace tk {
 namespace {
 
 constexpr int kBN = 64;     // keys per tile
-constexpr int kStages = 3;  // LDS stages (tile t read, t+1 read as "next K", t+2 landing)
+constexpr int kKSlots = 2;  // flash_dma_body K tiles in LDS: t+1 (read), t+2 (landing)
+constexpr int kVSlots = 3;  // flash_dma_body V tiles in LDS: t-1 (read), t, t+1 (landing)
 
-typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __fp16 hf16x2 __attribute__((ext_vector_type(2)));  // operand type of the fdot2 builtin
+typedef __fp16 tr_f16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) tr_f16x4 lds_tr_f16x4;
 
-// LDS byte offset of the 16-byte chunk `chunk` of row `row` in a tile whose
-// rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane accesses
-// for 16 lanes per cycle from one 256-byte line of 64 banks, so the chunk
-// index is XOR-ed with the row's line number (modulo the chunks per row):
-// 16 consecutive rows read at one logical chunk then hit 16 distinct 16-byte
-// bank groups.
+// LDS byte offset of the 16-byte chunk `chunk` of row `row` in a K tile
+// whose rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane
+// accesses for 16 lanes per cycle from one 256-byte line of 64 banks, so the
+// chunk index is XOR-ed with the row's line number (modulo the chunks per
+// row): 16 consecutive rows read at one logical chunk then hit 16 distinct
+// 16-byte bank groups.
 template <int RB>
 __device__ __forceinline__ int swz_off(int row, int chunk) {
   if constexpr (RB >= 256) return row * RB + ((chunk ^ (row & 15)) << 4);
@@ -52,11 +62,20 @@ __device__ __forceinline__ int swz_off(int row, int chunk) {
   else return row * RB + ((chunk ^ ((row >> 3) & 1)) << 4);
 }
 
+// Chunk XOR of a V tile row for the transposed reads: the four rows a
+// half-wave reads (r0..r0+3, r0 % 4 == 0) must put the 32 bytes each of them
+// contributes on distinct banks.  Rows of 64 or 32 bytes already do.
+template <int RB>
+__device__ __forceinline__ int vswz(int row) {
+  if constexpr (RB == 128) return 4 * ((row >> 1) & 1);
+  else return 0;
+}
+
 // Max / sum over the lane pair (l, l^32) that holds one query row.
 // v_permlane32_swap of a register with itself leaves, in every lane, its own
 // value in one half of the result and the partner's in the other, so a
 // symmetric op over both halves is the pair reduction -- two VALU ops, no
-// LDS round trip (a ds_bpermute would also wait on the in-flight K reads).
+// LDS round trip.
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -66,8 +85,31 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Position of key k (0..63 within the tile) in a V^T row: bits 2 and 3 swapped.
-__device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+// s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding).
+__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+
+// One 16-byte-per-lane global -> LDS copy of a wave (lane l lands at
+// lds_addr + 16*l).  Issued as inline assembly so that the compiler's wait
+// insertion, which cannot tell the ring slots apart, does not put a vmcnt(0)
+// in front of every later LDS read; the kernel waits for its copies itself
+// (wait_copies before each workgroup barrier).  M0 is saved and restored.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds_addr)
+      : "memory");
+}
+
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
 
 struct AttnArgs {
   const f16* q;
@@ -81,13 +123,374 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
 };
 
-// The body is a __device__ function (the __global__ wrapper below only calls
-// it): device-only builtins used directly in a kernel template's lambdas
-// would make the host-side instantiation, and with it the launch stub, fail.
-// KMASK: the key-validity mask p.kv is applied (a separate instantiation, so
-// the unmasked kernels carry none of its registers or loads).
+// ---- register-staged V (flash_vreg_body) ----
+constexpr int kStages = 3;  // LDS stages (tile t read, t+1 read as "next K", t+2 landing)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Position of key k (0..63 within the tile) in a V^T row: bits 2 and 3 swapped.
+__device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+// The bodies are __device__ functions (the __global__ wrapper below only
+// calls them): device-only builtins used directly in a kernel template's
+// lambdas would make the host-side instantiation, and with it the launch
+// stub, fail.  KMASK: the key-validity mask p.kv is applied (a separate
+// instantiation, so the unmasked kernels carry none of its registers or
+// loads).
 template <int HD, int NW, bool CAUSAL, bool KMASK>
-__device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
+__device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
+  constexpr int BM = 32 * NW;
+  constexpr int RB = HD * 2;               // K / V tile row bytes
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;           // bytes per K or V tile
+  constexpr int COPIES = TILE / 1024;      // 1 KB wave copies per tile
+  constexpr int CPW = (COPIES + NW - 1) / NW;
+  constexpr int RPC = 1024 / RB;           // tile rows per copy
+  constexpr int DB = (HD + 31) / 32;       // 32-row blocks of the O^T accumulator
+  constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
+  constexpr int NS = 2 * KSTEPS;           // S^T MFMAs per tile
+  constexpr int NP = 4 * DB;               // O^T MFMAs per tile
+  constexpr int NM = NS + NP;
+  constexpr int NC = NM / 2 < 4 ? 4 : NM / 2;  // chunks per step
+  constexpr int EPC = 32 / NC;             // score entries per lane per chunk
+  // chunk holding the last S^T MFMA, and the first chunk that reads its result
+  constexpr int C_LAST_S = [] {
+    int c = 0;
+    while (NS - 1 >= ((c + 1) * NM) / NC) ++c;
+    return c;
+  }();
+  constexpr int C_MAX = C_LAST_S + 2 < NC ? C_LAST_S + 2 : NC;
+  static_assert(HD <= 64, "head_dim 128 takes flash_vreg_body");
+  static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
+  static_assert(32 % NC == 0 && EPC % 2 == 0, "chunks must split the 32 entries into pairs");
+
+  __shared__ __attribute__((aligned(16))) char smem[(kKSlots + kVSlots) * TILE];
+  const uint32_t lds_base = (uint32_t)(size_t)(lds_char*)smem;
+  auto kslot = [&](int i) { return smem + i * TILE; };
+  auto vslot = [&](int i) { return smem + (kKSlots + i) * TILE; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = p.B * p.H;
+  const int n_qt = (p.S + BM - 1) / BM;
+  // Heaviest (last) query tiles first; bh fastest so that a head's tiles
+  // stay on one XCD (hardware ids are dealt round-robin over 8 XCDs).
+  const int id = blockIdx.x;
+  const int qt = CAUSAL ? (n_qt - 1 - id / BH) : id / BH;
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = qt * BM;
+
+  const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
+  const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
+  const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kvs : nullptr;
+
+  const int my_row = q0 + wave * 32 + (lane & 31);
+  const int g = lane >> 5;
+  const int wave_row_min = q0 + wave * 32;
+
+  // Q^T fragments (B operand): lane supplies Q[row][16*kk + 8*g .. +8].
+  f16x8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if (my_row < p.S)
+      qf[kk] = *reinterpret_cast<const f16x8*>(qb + (int64_t)my_row * p.qs[2] + kk * 16 + g * 8);
+    else
+      qf[kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  wait_copies();  // Q is in registers before any copy is issued
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[d][r] = 0.f;
+  float m_run = -INFINITY;  // running max of scale*log2e*s
+  float l_run = 0.f;        // lane-partial running sum (this lane's keys)
+
+  const int kv_end = CAUSAL ? min(p.S, q0 + BM) : p.S;
+  const int n_kt = (kv_end + kBN - 1) / kBN;
+
+  // ---- copies: lane sources within a tile are fixed; a tile adds 64 rows ----
+  // Lane l of wave copy ci writes physical chunk l % CPR of tile row
+  // ci*RPC + l / CPR and fetches the logical chunk the swizzle maps there.
+  int c_row[CPW], k_col[CPW], v_col[CPW];
+  const f16* k_src[CPW];
+  const f16* v_src[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int ci = wave + i * NW;
+    const int row = ci * RPC + lane / CPR;
+    const int phys = lane % CPR;
+    c_row[i] = row;
+    k_col[i] = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
+    v_col[i] = (phys ^ vswz<RB>(row)) * 8;
+    k_src[i] = kb + (int64_t)row * p.ks[2] + k_col[i];
+    v_src[i] = vb + (int64_t)row * p.vs[2] + v_col[i];
+  }
+  const int64_t k_tile = (int64_t)kBN * p.ks[2], v_tile = (int64_t)kBN * p.vs[2];
+  auto copy_tile = [&](const f16* const (&src)[CPW], const f16* base, int64_t rs, int64_t tstride,
+                       const int (&col)[CPW], int j, uint32_t dst) {
+    if ((j + 1) * kBN <= p.S) {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i)
+        if (COPIES % NW == 0 || wave + i * NW < COPIES)
+          dma16(src[i] + j * tstride, dst + (wave + i * NW) * 1024);
+    } else {  // last tile: rows past S re-read row S-1 (finite; masked or multiplied by P = 0)
+#pragma unroll
+      for (int i = 0; i < CPW; ++i)
+        if (COPIES % NW == 0 || wave + i * NW < COPIES) {
+          const int key = min(j * kBN + c_row[i], p.S - 1);
+          dma16(base + (int64_t)key * rs + col[i], dst + (wave + i * NW) * 1024);
+        }
+    }
+  };
+  auto copy_k = [&](int j) { copy_tile(k_src, kb, p.ks[2], k_tile, k_col, j, lds_base + (j % kKSlots) * TILE); };
+  auto copy_v = [&](int j) {
+    copy_tile(v_src, vb, p.vs[2], v_tile, v_col, j, lds_base + (kKSlots + j % kVSlots) * TILE);
+  };
+
+  // ---- operand reads ----
+  // A operand of S^T MFMA c (key block c / KSTEPS, k-step c % KSTEPS).
+  auto read_k = [&](const char* ks_, int c) {
+    return *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>((c / KSTEPS) * 32 + (lane & 31), 2 * (c % KSTEPS) + g));
+  };
+  // A operand of O^T MFMA c: P column block t = c / DB, head-dim block c % DB.
+  // lane = 16*q + s; read r (0/1) covers keys 16t + 8r + 4*(q >> 1) + (s >> 2)
+  // and head-dim columns 32*db + 16*(q & 1) + 4*(s & 3); the swizzle only sees
+  // row bits 0-1, which 16t leaves unchanged.
+  int v_rd[2][DB];
+  {
+    const int tq = lane >> 4, ts = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
+        const int col = 32 * d + (HD >= 32 ? 16 * (tq & 1) : 0) + 4 * (ts & 3);  // HD 16: lanes >= 16 are zeroed
+        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
+      }
+  }
+  const bool d_ok = HD % 32 == 0 || (lane & 31) < HD;  // head-dim row of this lane's O^T entries exists
+  auto read_v = [&](const char* vs_, int c) -> f16x8 {
+    const int t = c / DB, d = c % DB;
+    const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
+    const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
+    const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
+    const f16x8 f = __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2,
+                                            3, 4, 5, 6, 7);
+    return d_ok ? f : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  };
+  // O^T += V^T . P^T for a whole tile (rescale path and the last tile).
+  auto pv_all = [&](const f16x8 (&pf)[4], const char* vs_) {
+#pragma unroll
+    for (int c = 0; c < NP; ++c)
+      acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(vs_, c), pf[c / DB], acc_o[c % DB], 0, 0, 0);
+  };
+
+  // Key validity of a tile as one 64-bit ballot (bit j: key k0 + j valid).
+  // The byte of tile kt+1 is loaded at the start of step kt and turned into
+  // bits after the step's copy wait, so no wait for it lands mid-step.
+  auto key_byte = [&](int kt) { return KMASK ? (int)kvb[min(kt * kBN + lane, p.S - 1)] : 1; };
+  uint64_t kbits_cur = KMASK ? (uint64_t)__ballot(key_byte(0) != 0) : 0ull;
+  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
+
+  // One tile step kt (see the header).  accumulator entry r of block kb2 is
+  // key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4.
+  auto step = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], f16x8 (&p_cur)[4], f16x8 (&p_prev)[4],
+                  float& mx_cur, float& mx_next, auto next_c, auto prev_c) {
+    constexpr bool HAS_NEXT = decltype(next_c)::value;
+    constexpr bool HAS_PREV = decltype(prev_c)::value;
+    const int k0 = kt * kBN;
+    if (kt + 2 < n_kt) copy_k(kt + 2);
+    if (HAS_NEXT) copy_v(kt + 1);
+    int kbyte_next = 1;
+    if (KMASK && HAS_NEXT) kbyte_next = key_byte(kt + 1);
+
+    float mx = mx_cur;
+    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
+    if (need_mask) {
+      // bit j of kbits: key k0 + 4*g + j is valid
+      const uint64_t kbits = kbits_cur >> (4 * g);
+      mx = -INFINITY;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+          const int key = k0 + j + 4 * g;
+          if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kbits >> j) & 1) == 0))
+            s_cur[kb2][r] = -INFINITY;
+          mx = fmaxf(mx, s_cur[kb2][r]);
+        }
+    }
+    mx = pair_max(mx);
+    const float cs = p.scale_log2;
+    const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
+    // Lazy rescale: the reference max m_run only moves when some row of the
+    // wave has grown by more than 2^8 over it, so exponentials stay <= 256
+    // (exact in fp16's range) and the O/l rescale is skipped on most tiles;
+    // O and l always share one reference, so the final O/l is unchanged.
+    // The pending P of tile kt-1 is relative to the old reference: it is
+    // accumulated first and its deferred MFMAs below then add zeros.
+    if (__any(m_tile > m_run + 8.0f)) {
+      if (HAS_PREV) {
+        pv_all(p_prev, vslot((kt + kVSlots - 1) % kVSlots));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) p_prev[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+
+    // ---- chunks: MFMAs m in [c*NM/NC, (c+1)*NM/NC): S^T(kt+1) first, then O^T(kt-1) ----
+    const char* ks_n = kslot((kt + 1) % kKSlots);
+    const char* vs_p = vslot((kt + kVSlots - 1) % kVSlots);
+    f16x8 frag[NM];
+    auto issue_read = [&](int m) {
+      if (m < NS) {
+        if (HAS_NEXT) frag[m] = read_k(ks_n, m);
+      } else if (m < NM) {
+        if (HAS_PREV) frag[m] = read_v(vs_p, m - NS);
+      }
+    };
+    auto do_mfma = [&](int m) {
+      if (m < NS) {
+        if (HAS_NEXT) {
+          const int kb2 = m / KSTEPS, kk = m % KSTEPS;
+          s_next[kb2] =
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], qf[kk], kk == 0 ? f32x16{} : s_next[kb2], 0, 0, 0);
+        }
+      } else if (HAS_PREV) {
+        const int c = m - NS;
+        acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], p_prev[c / DB], acc_o[c % DB], 0, 0, 0);
+      }
+    };
+    float pe[32];
+    float ls = 0.f;
+    auto exp_entry = [&](int e) {
+      pe[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], cs, -m_use));
+      if (e & 1) {
+        const f16x2 hp = {(f16)pe[e - 1], (f16)pe[e]};
+        p_cur[e >> 3][(e & 7) - 1] = hp[0];
+        p_cur[e >> 3][e & 7] = hp[1];
+        ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+      }
+    };
+    float mxn = -INFINITY;
+    // Reads run three MFMAs ahead of their use.
+    constexpr int RA = 3;
+#pragma unroll
+    for (int m = 0; m < RA && m < NM; ++m) issue_read(m);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int m0 = (c * NM) / NC, m1 = ((c + 1) * NM) / NC;
+      const int e0 = c * EPC, e1 = (c + 1) * EPC;
+#pragma unroll
+      for (int m = m0; m < m1; ++m) {
+        if (m + RA < NM) issue_read(m + RA);
+        do_mfma(m);
+        // exponentials split evenly over the chunk's MFMAs
+        const int ea = e0 + ((m - m0) * EPC) / (m1 - m0), eb = e0 + ((m - m0 + 1) * EPC) / (m1 - m0);
+#pragma unroll
+        for (int e = ea; e < eb; ++e) exp_entry(e);
+      }
+      if (m1 == m0) {
+#pragma unroll
+        for (int e = e0; e < e1; ++e) exp_entry(e);
+      }
+      // row max of S(kt+1), spread over the chunks after its last MFMA
+      if (HAS_NEXT && c >= C_MAX) {
+        const int n = NC - C_MAX;
+        const int a = ((c - C_MAX) * 32) / n, z = ((c - C_MAX + 1) * 32) / n;
+#pragma unroll
+        for (int e = a; e < z; ++e) mxn = fmaxf(mxn, s_next[e >> 4][e & 15]);
+      }
+    }
+    if (HAS_NEXT && C_MAX >= NC) {
+#pragma unroll
+      for (int e = 0; e < 32; ++e) mxn = fmaxf(mxn, s_next[e >> 4][e & 15]);
+    }
+    mx_next = mxn;
+    l_run += ls;
+    // keep the copy wait after every MFMA and read of the step
+    __builtin_amdgcn_sched_barrier(0);
+    wait_copies();
+    if (KMASK && HAS_NEXT) kbits_cur = (uint64_t)__ballot(kbyte_next != 0);
+    __syncthreads();
+  };
+
+  // ---- prologue: K(0), K(1), V(0) copied; S(0) and its row max ----
+  copy_k(0);
+  if (n_kt > 1) copy_k(1);
+  copy_v(0);
+  wait_copies();
+  __syncthreads();
+
+  f32x16 s_a[2], s_b[2];
+  f16x8 pf_a[4], pf_b[4];
+  float mx_a = -INFINITY, mx_b = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NS; ++c) {
+    const int kb2 = c / KSTEPS, kk = c % KSTEPS;
+    s_a[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(kslot(0), c), qf[kk],
+                                                      kk == 0 ? f32x16{} : s_a[kb2], 0, 0, 0);
+  }
+#pragma unroll
+  for (int e = 0; e < 32; ++e) mx_a = fmaxf(mx_a, s_a[e >> 4][e & 15]);
+  __syncthreads();  // K(0) read by every wave before step 0 refills its slot
+
+  const BoolC<true> T{};
+  const BoolC<false> F{};
+  if (n_kt == 1) {
+    step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, F);
+    pv_all(pf_a, vslot(0));
+  } else {
+    step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, F);
+    for (int kt = 1; kt < n_kt - 1; kt += 2) {
+      step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
+      if (kt + 1 < n_kt - 1) step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
+    }
+    const int kl = n_kt - 1;
+    if (kl & 1) {
+      step(kl, s_b, s_a, pf_b, pf_a, mx_b, mx_a, F, T);
+      pv_all(pf_b, vslot(kl % kVSlots));
+    } else {
+      step(kl, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, T);
+      pv_all(pf_a, vslot(kl % kVSlots));
+    }
+  }
+
+  // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
+  l_run = pair_sum(l_run);
+  const float inv = 1.0f / l_run;
+  if (my_row < p.S) {
+    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int dd = d * 32 + 8 * q + 4 * g;
+        if (dd < HD) {
+          f16x4 t = {(f16)(acc_o[d][4 * q] * inv), (f16)(acc_o[d][4 * q + 1] * inv),
+                     (f16)(acc_o[d][4 * q + 2] * inv), (f16)(acc_o[d][4 * q + 3] * inv)};
+          *reinterpret_cast<f16x4*>(ob + dd) = t;
+        }
+      }
+  }
+}
+
+template <int HD, int NW, bool CAUSAL, bool KMASK>
+__device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   constexpr int BM = 32 * NW;
   constexpr int NT = NW * 64;
   constexpr int KRB = HD * 2;               // K tile row bytes
@@ -365,9 +768,9 @@ __device__ __forceinline__ void flash_fwd_body(const AttnArgs& p) {
 
 template <int HD, int NW, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(AttnArgs p) {
-  flash_fwd_body<HD, NW, CAUSAL, KMASK>(p);
+  if constexpr (HD <= 64) flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
+  else flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
 }
-
 template <int HD, int NW>
 int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   constexpr int BM = 32 * NW;

@@ -428,7 +428,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
     asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
     constexpr int TOT = JC * 32 * CPR;
     static_assert(TOT % 64 == 0, "whole read-back passes");
-#pragma unroll
+    // Partial unroll: a fully unrolled read-back makes the enclosing jb loop
+    // too large to unroll, and acc[i][jb + jj] would then be indexed at run
+    // time, which puts the whole accumulator in scratch memory.
+#pragma unroll 4
     for (int idx0 = 0; idx0 < TOT; idx0 += 64) {
       const int idx = idx0 + lane;
       const int row = idx / CPR, ch = idx % CPR;

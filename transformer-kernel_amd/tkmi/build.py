@@ -9,13 +9,20 @@ Every ``csrc/*.hip`` file is compiled to an object under
 ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the compiler from
 emitting packed-fp32 VALU instructions (the host pass warns that it does not
 know the feature; that is harmless).
+
+The compiler's per-kernel resource report (registers, scratch, occupancy,
+LDS) is saved to ``_build/resource_usage.json``; the host tests check that
+the kernels on the benchmarked paths use no scratch memory (a spilled
+accumulator makes a kernel several times slower without changing results).
 """
 
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
 import pathlib
+import re
 import shutil
 import subprocess
 import sys
@@ -27,6 +34,7 @@ CSRC = ROOT / "csrc"
 INCLUDE = REPO / "include"
 BUILD_DIR = ROOT / "_build"
 LIB_PATH = PKG_DIR / "libtkmi.so"
+RESOURCE_PATH = BUILD_DIR / "resource_usage.json"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -48,13 +56,31 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: pathlib.Path) -> pathlib.Path:
+_REMARK = re.compile(r"remark: +(Function Name|TotalSGPRs|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]): (\S+)")
+_FIELDS = {"TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch",
+           "Occupancy [waves/SIMD]": "occupancy", "LDS Size [bytes/block]": "lds"}
+
+
+def _resource_usage(stderr: str) -> dict:
+    """Per-kernel figures from hipcc's -Rpass-analysis=kernel-resource-usage remarks."""
+    usage, cur = {}, None
+    for m in _REMARK.finditer(stderr):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = usage.setdefault(val, {})
+        elif cur is not None:
+            cur[_FIELDS[key]] = int(val)
+    return usage
+
+
+def _compile(src: pathlib.Path):
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr[-4000:]}")
-    return obj
+    return obj, _resource_usage(proc.stderr)
 
 
 def build(verbose: bool = True, jobs: int = 0) -> pathlib.Path:
@@ -65,7 +91,12 @@ def build(verbose: bool = True, jobs: int = 0) -> pathlib.Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, srcs))
+        results = list(pool.map(_compile, srcs))
+    objs = [obj for obj, _ in results]
+    usage = {}
+    for _, u in results:
+        usage.update(u)
+    RESOURCE_PATH.write_text(json.dumps(usage, indent=1, sort_keys=True))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
