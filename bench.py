@@ -2,11 +2,16 @@
 """Benchmark of the MI355X transformer-layer forward (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--config C2] [--no-cpu-baseline]
+    python bench.py --shape 64,128,128,4,128,4,causal [--dtype float16]
 
 A "step" is one forward of the whole layer stack over one batch of
-synthetic input (weights: torch.manual_seed(1234) construction; input: CPU
+synthetic input (weights: torch.manual_seed(1234) construction of the
+module tree, src/torch_transformer_benchmark.py:683-699; input: CPU
 generator seed 1234 + 100000, as the reference harness's timing input,
 src/torch_transformer_benchmark.py:529-536), with x already resident in HBM.
+``--shape B,S,D,H,F,L[,causal]`` times any shape; ``--dtype`` sets the model
+and input dtype as the harness's --dtype does
+(src/torch_transformer_benchmark.py:609-613, 698-699).
 W untimed steps, then K steps bracketed by torch.cuda.synchronize(); the
 per-step time is the median of per-step HIP-event samples
 (src/torch_transformer_benchmark.py:487-499,564).
@@ -21,7 +26,9 @@ second pass of K steps.
 
 ``cpu_baseline`` times the fp32 CPU oracle (a restatement of the reference's
 BaselineTransformer) on this host's cores for a bounded sample of the same
-workload.
+workload; where that sample is the whole timed forward (C1, C2 and shapes of
+that size) its output also checks the GPU forward's (``parity``, the
+harness's element rule).  The oracle is used by that leg only.
 """
 
 from __future__ import annotations
@@ -115,19 +122,92 @@ def measured_traffic(config: str, kernel: str):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+def parse_shape(text: str) -> tuple:
+    """``B,S,D,H,F,L[,causal|noncausal]`` -> (B, S, D, H, F, L, causal)."""
+    parts = [t.strip() for t in text.split(",") if t.strip()]
+    if len(parts) not in (6, 7):
+        raise SystemExit(f"--shape wants B,S,D,H,F,L[,causal|noncausal], got {text!r}")
+    nums = tuple(int(t) for t in parts[:6])
+    causal = True if len(parts) == 6 else parts[6].lower() in ("causal", "c", "1", "true")
+    return nums + (causal,)
+
+
+# CPU work (fp32 flop) above which the CPU leg is skipped instead of sampled.
+CPU_FLOP_CAP = 4e12
+
+
+def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str):
+    """Time the fp32 CPU oracle on a bounded sample of the workload; when the
+    sample is the whole forward, also check the GPU output against it.
+    Returns (cpu_baseline dict or None, parity dict or None)."""
+    from oracle import baseline as ob  # the CPU baseline and its parity check only
+
+    b, s, d, h, f, nl, causal = cfg_t
+    cfg = ob.TransformerConfig(b, s, d, h, f, nl, causal)
+    base = ob.BaselineTransformer(cfg)
+    state = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    base.load_state_dict(state, strict=True)
+    base = base.eval()
+    cores = cpu_cores()
+    torch.set_num_threads(cores)
+    pairs = s * (s + 1) / 2 if causal else s * s
+    flop_per_sample = nl * (2 * s * (4 * d * d + 2 * d * f) + 4 * d * pairs)
+    full = b * h * s * s * 4 <= 2 ** 31 and b * flop_per_sample <= CPU_FLOP_CAP
+    xs_full = x_host.float()
+    parity = None
+    if full:
+        fn = None
+        xs, sample_b = xs_full, b
+        sample = f"full {label} forward (B{b} S{s}), median of 3 after 1 warmup"
+        reps, warm = 3, 1
+    elif flop_per_sample <= CPU_FLOP_CAP:
+        xs, sample_b = xs_full[:1], 1
+        fn = lambda t: ob.chunked_forward(base, t, q_chunk=2048)  # noqa: E731
+        sample = f"query-chunked fp32 oracle, batch 1 of {b}, x{b} scaled; 1 repeat after 0 warmup"
+        reps, warm = 1, 0
+    else:
+        return None, None
+    ts = ob.time_cpu_forward(base, xs, warmup=warm, repeats=reps, fn=fn)
+    cpu_fwd = statistics.median(ts) * (b / sample_b)
+    cpu = {
+        "value": round(cpu_fwd / nl, 3),
+        "unit": "ms",
+        "cores": cores,
+        "kind": "port",
+        "sample": sample,
+        "forward_ms": round(cpu_fwd, 2),
+    }
+    if full and out_gpu is not None:
+        with torch.inference_mode():
+            ref = base(xs)
+        r = ob.compare_outputs(ref, out_gpu)
+        parity = {"passed": r.passed, "max_abs": r.max_abs_error, "failed": r.failed_elements,
+                  "elements": r.total_elements, "input": "the timed input (seed 101234)"}
+        print(f"[bench] parity {label}: {'PASS' if r.passed else 'FAIL'} max_abs={r.max_abs_error:.3g}",
+              file=sys.stderr, flush=True)
+    return cpu, parity
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
+    ap.add_argument("--shape", default=None,
+                    help="B,S,D,H,F,L[,causal|noncausal] instead of --config (causal by default)")
+    ap.add_argument("--dtype", default="float32", choices=("float32", "float16", "bfloat16"),
+                    help="model and input dtype, as the reference harness's --dtype")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-check", action="store_true", help="skip the one-trial parity check")
+    ap.add_argument("--no-check", action="store_true", help="skip the parity check of the CPU-baseline leg")
     ap.add_argument("--graph", action="store_true",
                     help="time the whole forward replayed from a HIP graph (tkmi.graphs.GraphedTransformer)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of COPY_BYTES (torch copy_), the reference kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    ap.add_argument("--dispatch", nargs="?", const="default", default=None,
+                    help="apply the per-shape settings table (tkmi/configs/dispatch.json, or the path given); "
+                         "--graph / --unfused-norm given here win")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -148,42 +228,44 @@ def main() -> int:
 
     import tkmi
     from tkmi import ops
-    from oracle import baseline as ob  # parity check and cpu_baseline only
 
-    cfg_t = CONFIGS[args.config]
+    if args.shape:
+        cfg_t = parse_shape(args.shape)
+        workload = "shape"
+    else:
+        cfg_t = CONFIGS[args.config]
+        workload = args.config
     b, s, d, h, f, nl, causal = cfg_t
-    cfg = ob.TransformerConfig(b, s, d, h, f, nl, causal)
+    dtype = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[args.dtype]
     dev = torch.device("cuda:0")
     torch.set_num_threads(cpu_cores())
     torch.set_float32_matmul_precision("highest")
 
-    base = ob.build_model(cfg, seed=1234).eval()
+    chosen = None
+    if args.dispatch:
+        from tkmi import dispatch as tkd
+
+        chosen = tkd.settings_for(tkd.load_table(None if args.dispatch == "default" else args.dispatch), *cfg_t)
+        if chosen:
+            args.graph = args.graph or chosen["graph"]
+            args.unfused_norm = args.unfused_norm or not chosen["fused_norm"]
     settings = tkmi.OptimizerSettings(fused_norm=not args.unfused_norm)
-    model = tkmi.OptimizedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
-    ob.copy_model_weights(base, model, strict=True)
-    model = model.to(dev).eval()
-    timed_model = model
+    cls = tkmi.OptimizedTransformer
     if args.graph:
-        from tkmi.graphs import GraphedTransformer
+        from tkmi.graphs import GraphedTransformer as cls
+    torch.manual_seed(1234)  # the harness's construction order and seed
+    model = cls(tkmi.TransformerConfig(*cfg_t), settings).to(device=dev, dtype=dtype).eval()
+    timed_model = model
+    eager = model
+    if args.graph:  # built here, outside inference mode: its parameters are ordinary tensors
+        eager = tkmi.OptimizedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
+        eager.load_state_dict(model.state_dict())
+        eager = eager.to(device=dev, dtype=dtype).eval()
 
-        timed_model = GraphedTransformer(tkmi.TransformerConfig(*cfg_t), settings)
-        ob.copy_model_weights(base, timed_model, strict=True)
-        timed_model = timed_model.to(dev).eval()
-
-    parity = None
-    if not args.no_check and args.config in ("C1", "C2"):
-        x_chk, m_chk = ob.generate_random_case(cfg, seed=1234)
-        with torch.inference_mode():
-            got = model(x_chk.to(dev), m_chk.to(dev)).cpu()
-            ref = base(x_chk, m_chk)
-        r = ob.compare_outputs(ref, got)
-        parity = {"passed": r.passed, "max_abs": r.max_abs_error, "failed": r.failed_elements,
-                  "elements": r.total_elements, "trial_seed": 1234}
-        print(f"[bench] parity {args.config}: {'PASS' if r.passed else 'FAIL'} max_abs={r.max_abs_error:.3g}",
-              file=sys.stderr, flush=True)
-        del x_chk, m_chk, got, ref
-
-    x, mask = ob.generate_random_case(cfg, seed=1234 + 100000)
+    gen = torch.Generator().manual_seed(1234 + 100000)
+    x = torch.randn(b, s, d, generator=gen).to(dtype)
+    mask = torch.ones(b, s, dtype=torch.bool)
+    x_host = x
     x, mask = x.to(dev), mask.to(dev)
 
     with torch.inference_mode():
@@ -202,11 +284,13 @@ def main() -> int:
         samples = [a.elapsed_time(e) for a, e in zip(starts, ends)]
         print(f"[bench] timed {args.steps} steps in {wall:.3f}s", file=sys.stderr, flush=True)
 
-        # Per-kernel durations: events around each launch, on the launch stream.
+        # Per-kernel durations: events around each launch, on the launch stream
+        # (the eager forward: a replayed graph records no per-launch events).
         with ops.kernel_timer() as rec:
             for _ in range(args.steps):
-                model(x, mask)
+                eager(x, mask)
             torch.cuda.synchronize()
+        got_gpu = model(x, mask).float().cpu() if not args.no_cpu_baseline and not args.no_check else None
         per = {}
         for name, e0, e1 in rec:
             per.setdefault(name, []).append(e0.elapsed_time(e1))
@@ -241,35 +325,13 @@ def main() -> int:
         "peak": PEAK_FP16_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBPS,
         "unit": dom["unit"],
         "frac": dom["frac"],
-        "traffic": measured_traffic(args.config, dom_name),
+        "traffic": measured_traffic(workload, dom_name) if args.dtype == "float32" else None,
     }
 
-    cpu = None
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
-        cores = cpu_cores()
-        torch.set_num_threads(cores)
-        if args.config in ("C4", "C5"):
-            sample_b = 1
-            xs, _ = ob.generate_random_case(ob.TransformerConfig(1, s, d, h, f, nl, causal), seed=101234)
-            fn = lambda t: ob.chunked_forward(base, t, q_chunk=2048)  # noqa: E731
-            sample = f"query-chunked fp32 oracle, batch 1 of {b}, x{b} scaled; 1 repeat after 0 warmup"
-            reps, warm = 1, 0
-        else:
-            sample_b = b
-            xs = x.cpu()
-            fn = None
-            sample = f"full {args.config} forward (B{b} S{s}), median of 3 after 1 warmup"
-            reps, warm = 3, 1
-        ts = ob.time_cpu_forward(base, xs, warmup=warm, repeats=reps, fn=fn)
-        cpu_fwd = statistics.median(ts) * (b / sample_b)
-        cpu = {
-            "value": round(cpu_fwd / nl, 3),
-            "unit": "ms",
-            "cores": cores,
-            "kind": "port",
-            "sample": sample,
-            "forward_ms": round(cpu_fwd, 2),
-        }
+        cpu, parity = cpu_baseline_leg(model, cfg_t, x_host, out_gpu=None if args.no_check else got_gpu,
+                                       label=workload)
 
     t = b * s
     line = {
@@ -284,12 +346,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16 operands, fp32 accumulate / residual / statistics",
+        "input_dtype": args.dtype,
         "data": "synthetic (seeded randn input, seeded nn.Linear default init)",
         "config": {
-            "workload": f"{args.config}: B{b} S{s} D{d} H{h} F{f} L{nl} {'causal' if causal else 'non-causal'}",
+            "workload": f"{workload}: B{b} S{s} D{d} H{h} F{f} L{nl} {'causal' if causal else 'non-causal'}",
             "batch": b, "seq_len": s, "d_model": d, "heads": h, "ffn_dim": f, "layers": nl,
             "causal": causal, "parallelism": "single GPU", "fused_norm": not args.unfused_norm,
-            "hip_graph": bool(args.graph),
+            "hip_graph": bool(args.graph), "dispatch": chosen,
         },
         "tokens_per_s": round(t * 1000.0 / fwd_ms, 1),
         "wall_s_timed": round(wall, 4),

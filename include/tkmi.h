@@ -142,7 +142,7 @@ int tk_gemm_ln_supported(int64_t n);
  * like future keys (src/torch_transformer_benchmark.py:104-107).  A query
  * row with no valid key yields non-finite output (the baseline's NaN row);
  * callers zero such padded rows downstream.
- * head_dim in {16, 32, 64, 128} (tk_attention_supported).
+ * head_dim in {16, 32, 64, 128, 256} (tk_attention_supported).
  * Replaces kernels.flash_attention / _flash_attn_fwd_kernel
  * (src/kernels.py:250-294, :137-247) and F.scaled_dot_product_attention
  * (src/optimized.py:615-626).

@@ -252,6 +252,8 @@ ATTN_SHAPES = [  # (B, H, S, hd); the reference's shapes with a supported head_d
     (8, 16, 512, 64),   # 128-row tile path
     (1, 2, 1024, 128),
     (4, 8, 64, 64),     # C2-like: one key tile per head
+    (1, 2, 64, 256),
+    (2, 3, 700, 256),   # head_dim 256, 4-wave tiles, ragged last tile
 ]
 
 
@@ -374,7 +376,8 @@ def test_flash_attention_key_mask(shape, causal):
 def test_attention_support_probes():
     assert ops.attention_supported(64, torch.float16, DEV)
     assert not ops.attention_supported(8, torch.float16, DEV)
-    assert not ops.attention_supported(256, torch.float16, DEV)
+    assert ops.attention_supported(256, torch.float16, DEV)
+    assert not ops.attention_supported(512, torch.float16, DEV)
     assert not ops.attention_supported(64, torch.float32, DEV)
     q = torch.zeros(1, 1, 8, 8, dtype=torch.float16, device=DEV)
     with pytest.raises(_lib.TkError, match="head_dim"):

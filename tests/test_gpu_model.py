@@ -234,3 +234,58 @@ def test_graphed_forward_replays_match_eager():
         replayed = graphed(inputs[1], mask).cpu()
         ref = base(inputs[1].cpu(), mask.cpu())
     assert ob.compare_outputs(ref, replayed).passed
+
+
+# Head dims without a kernel tile run zero-padded to the next one (16/32/64/128/256):
+# 8 is appendix case 7's (d_model 32, 4 heads).
+@pytest.mark.parametrize("shape", [(8, 64, 32, 4, 64, 2, True), (2, 96, 96, 4, 192, 2, False),
+                                   (2, 160, 192, 4, 256, 1, True), (1, 300, 320, 4, 512, 1, True),
+                                   (2, 130, 800, 4, 256, 1, True)])
+def test_padded_head_dims(shape):
+    cfg = ob.TransformerConfig(*shape)
+    base, opt = _pair(cfg)
+    assert opt.head_dim_padded in (16, 32, 64, 128, 256) and opt.head_dim_padded > opt.head_dim
+    x, mask = ob.generate_random_case(cfg, seed=21)
+    with torch.inference_mode():
+        got = opt(x.to(DEV), mask.to(DEV)).cpu()
+        ref = base(x, mask)
+    res = ob.compare_outputs(ref, got)
+    _report(f"head_dim {opt.head_dim} -> {opt.head_dim_padded}", res)
+    assert res.passed
+
+
+# The harness's --dtype runs model and input in fp16/bf16
+# (src/torch_transformer_benchmark.py:609-613, 698-699); the output keeps that dtype.
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_precision_models_and_inputs(dtype):
+    cfg = ob.TransformerConfig(4, 128, 256, 4, 512, 2, True)
+    torch.manual_seed(1234)
+    opt = tkmi.OptimizedTransformer(tkmi.TransformerConfig(**cfg.__dict__)).to(device=DEV, dtype=dtype).eval()
+    base = ob.BaselineTransformer(cfg)
+    base.load_state_dict({k: v.float().cpu() for k, v in opt.state_dict().items()}, strict=True)
+    base.eval()
+    x, mask = ob.generate_random_case(cfg, seed=5)
+    xd = x.to(dtype)
+    with torch.inference_mode():
+        got = opt(xd.to(DEV), mask.to(DEV))
+        ref = base(xd.float(), mask)
+    assert got.dtype == dtype
+    res = ob.compare_outputs(ref, got.float().cpu())
+    _report(f"{dtype}", res)
+    assert res.passed
+
+
+# head_dim 256 (appendix case 8: d_model 1024, 4 heads) has its own tile.
+@pytest.mark.parametrize("shape", [(4, 128, 1024, 4, 1024, 2, True), (2, 200, 512, 2, 512, 1, False),
+                                   (1, 64, 256, 1, 256, 1, True)])
+def test_head_dim_256(shape):
+    cfg = ob.TransformerConfig(*shape)
+    base, opt = _pair(cfg)
+    assert opt.head_dim == 256 and opt.head_dim_padded == 256
+    x, mask = ob.generate_random_case(cfg, seed=8)
+    with torch.inference_mode():
+        got = opt(x.to(DEV), mask.to(DEV)).cpu()
+        ref = base(x, mask)
+    res = ob.compare_outputs(ref, got)
+    _report(f"head_dim 256 {shape}", res)
+    assert res.passed

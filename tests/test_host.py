@@ -126,7 +126,7 @@ def test_every_kernel_has_a_launch_stub():
 
 def test_capability_probes():
     lib = _lib.load()
-    assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256)] == [0, 1, 1, 1, 1, 0]
+    assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256, 512)] == [0, 1, 1, 1, 1, 1, 0]
     assert [lib.tk_gemm_ln_supported(n) for n in (64, 128, 256, 512, 1024)] == [0, 1, 1, 1, 0]
 
 
@@ -193,3 +193,69 @@ def test_hot_kernels_use_no_scratch():
     assert not missing, missing
     spilled = {k: usage[k]["scratch"] for k in hot if usage[k].get("scratch", 0) > 0}
     assert not spilled, spilled
+
+
+# ---------------------------------------------------------------- tooling --
+
+def test_bench_parse_shape():
+    import bench
+
+    assert bench.parse_shape("64,128,128,4,128,4") == (64, 128, 128, 4, 128, 4, True)
+    assert bench.parse_shape("2, 64, 512, 8, 2048, 4, noncausal") == (2, 64, 512, 8, 2048, 4, False)
+    with pytest.raises(SystemExit):
+        bench.parse_shape("1,2,3")
+
+
+def test_sweep_commands_and_records():
+    from tkmi import sweep
+
+    case = {"id": 1, "batch_size": 64, "seq_len": 128, "d_model": 128, "heads": 4, "ffn_dim": 128, "layers": 4,
+            "causal": True, "extra_args": ["--graph"]}
+    cmd = sweep.case_command(case, ["--steps", "5"])
+    assert cmd[1].endswith("bench.py") and cmd[2:4] == ["--shape", "64,128,128,4,128,4,causal"]
+    assert cmd[-3:] == ["--steps", "5", "--graph"]  # passthrough first, then the case's own flags
+    long_case = dict(case, id=14, runner="longseq", extra_args=[])
+    assert sweep.case_command(long_case, ["--steps", "5"])[1:3] == ["-m", "tkmi.longseq"]
+    line = {"ms_per_step": 0.25, "tokens_per_s": 3.2e7, "value": 0.0625, "roofline": {"frac": 0.1},
+            "input_dtype": "float32", "device": "gpu", "cpu_baseline": {"forward_ms": 50.0, "cores": 16, "sample": "s"},
+            "parity": {"passed": True, "max_abs": 1e-3, "failed": 0, "elements": 10}}
+    rec = sweep.parse_result(case, sweep._last_json("noise\n" + json.dumps(line) + "\n"))
+    assert rec["optimized"]["median_ms"] == 0.25 and rec["speedup"] == 200.0
+    assert rec["accuracy"]["passed"] and sweep.classify(0, rec, False) == "ok"
+    bad = dict(rec, accuracy=dict(rec["accuracy"], passed=False))
+    assert sweep.classify(0, bad, False) == "accuracy_failed"
+    assert sweep.classify(1, rec, False) == "error" and sweep.classify(0, rec, True) == "timeout"
+    assert sweep.classify(0, {}, False) == "error"
+
+
+def test_dispatch_table_keeps_fastest_passing_run(tmp_path):
+    from tkmi import dispatch
+
+    case = {"id": 1, "batch_size": 64, "seq_len": 128, "d_model": 128, "heads": 4, "ffn_dim": 128, "layers": 4,
+            "causal": True}
+    def results(name, passthrough, ms, status="ok"):
+        path = tmp_path / name
+        path.write_text(json.dumps({"schema": 1, "passthrough_args": passthrough,
+                                    "cases": [{"case": case, "status": status, "optimized": {"median_ms": ms}}]}))
+        return path
+    paths = [results("eager.json", [], 0.27), results("graph.json", ["--graph"], 0.12),
+             results("broken.json", ["--unfused-norm"], 0.01, status="accuracy_failed")]
+    table = dispatch.build_table(paths)
+    assert len(table["shapes"]) == 1
+    entry = table["shapes"][0]
+    assert entry["settings"] == {"graph": True, "fused_norm": True} and entry["median_ms"] == 0.12
+    assert dispatch.settings_for(table, 64, 128, 128, 4, 128, 4, True) == {"graph": True, "fused_norm": True}
+    assert dispatch.settings_for(table, 64, 128, 128, 4, 128, 4, False) is None
+
+
+def test_shape_tables_are_well_formed():
+    from tkmi import sweep
+
+    for name in ("shapes.json", "baseline.json"):
+        table = json.loads((sweep.PKG / "configs" / name).read_text())
+        ids = [c["id"] for c in table["cases"]]
+        assert len(ids) == len(set(ids))
+        for c in table["cases"]:
+            assert c["d_model"] % c["heads"] == 0
+    appendix = json.loads((sweep.PKG / "configs" / "shapes.json").read_text())["cases"]
+    assert len(appendix) == 14 and appendix[-1]["runner"] == "longseq"

@@ -15,12 +15,13 @@
 //     the keys {16t + 8*e2 + 4g + e10} (g = lane >> 5).
 //
 // Two bodies, picked by head_dim at compile time:
-//   flash_dma_body (head_dim <= 64): K and V tiles copied global -> LDS
+//   flash_dma_body (head_dim <= 64, and 256): K and V tiles copied global -> LDS
 //     directly (global_load_lds_dwordx4, row-major); the V^T operand is two
 //     ds_read_b64_tr_b16 of the row-major V tile.  The O^T MFMAs of tile t-1
 //     are deferred into step t, so every MFMA of a step is independent of
 //     the step's exponentials and interleaves with them; the row max of the
-//     next tile is computed in the same pass.
+//     next tile is computed in the same pass.  At head_dim 256 (one wave per
+//     SIMD, 4-wave workgroups) tile t's O^T MFMAs run at the end of step t.
 //   flash_vreg_body (head_dim 128): the deferred P needs 16 more registers
 //     than two waves per SIMD leave at head_dim 128, so tile t's O^T MFMAs
 //     follow its exponentials; V^T is written to LDS from registers with
@@ -41,7 +42,6 @@ namespace {
 
 constexpr int kBN = 64;     // keys per tile
 constexpr int kKSlots = 2;  // flash_dma_body K tiles in LDS: t+1 (read), t+2 (landing)
-constexpr int kVSlots = 3;  // flash_dma_body V tiles in LDS: t-1 (read), t, t+1 (landing)
 
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __fp16 hf16x2 __attribute__((ext_vector_type(2)));  // operand type of the fdot2 builtin
@@ -67,7 +67,8 @@ __device__ __forceinline__ int swz_off(int row, int chunk) {
 // contributes on distinct banks.  Rows of 64 or 32 bytes already do.
 template <int RB>
 __device__ __forceinline__ int vswz(int row) {
-  if constexpr (RB == 128) return 4 * ((row >> 1) & 1);
+  if constexpr (RB >= 256) return 4 * (row & 3);
+  else if constexpr (RB == 128) return 4 * ((row >> 1) & 1);
   else return 0;
 }
 
@@ -150,7 +151,13 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
   constexpr int NS = 2 * KSTEPS;           // S^T MFMAs per tile
   constexpr int NP = 4 * DB;               // O^T MFMAs per tile
-  constexpr int NM = NS + NP;
+  // head_dim <= 64: the O^T MFMAs of tile t-1 are deferred into step t (V
+  // tiles t-1, t, t+1 in LDS).  head_dim 256 (one wave per SIMD, no room for
+  // the pending P's operands beside a 256-wide O accumulator) runs tile t's
+  // O^T MFMAs at the end of step t (V tiles t, t+1).
+  constexpr bool DEFER = HD <= 64;
+  constexpr int kVSlots = DEFER ? 3 : 2;
+  constexpr int NM = NS + (DEFER ? NP : 0);  // MFMAs of the interleaved chunk region
   constexpr int NC = NM / 2 < 4 ? 4 : NM / 2;  // chunks per step
   constexpr int EPC = 32 / NC;             // score entries per lane per chunk
   // chunk holding the last S^T MFMA, and the first chunk that reads its result
@@ -160,7 +167,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     return c;
   }();
   constexpr int C_MAX = C_LAST_S + 2 < NC ? C_LAST_S + 2 : NC;
-  static_assert(HD <= 64, "head_dim 128 takes flash_vreg_body");
+  static_assert(HD <= 64 || HD == 256, "head_dim 128 takes flash_vreg_body");
   static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
   static_assert(32 % NC == 0 && EPC % 2 == 0, "chunks must split the 32 entries into pairs");
 
@@ -336,7 +343,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     // The pending P of tile kt-1 is relative to the old reference: it is
     // accumulated first and its deferred MFMAs below then add zeros.
     if (__any(m_tile > m_run + 8.0f)) {
-      if (HAS_PREV) {
+      if (DEFER && HAS_PREV) {
         pv_all(p_prev, vslot((kt + kVSlots - 1) % kVSlots));
 #pragma unroll
         for (int t = 0; t < 4; ++t) p_prev[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -360,7 +367,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       if (m < NS) {
         if (HAS_NEXT) frag[m] = read_k(ks_n, m);
       } else if (m < NM) {
-        if (HAS_PREV) frag[m] = read_v(vs_p, m - NS);
+        if (DEFER && HAS_PREV) frag[m] = read_v(vs_p, m - NS);
       }
     };
     auto do_mfma = [&](int m) {
@@ -370,7 +377,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
           s_next[kb2] =
               __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], qf[kk], kk == 0 ? f32x16{} : s_next[kb2], 0, 0, 0);
         }
-      } else if (HAS_PREV) {
+      } else if (DEFER && HAS_PREV) {
         const int c = m - NS;
         acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], p_prev[c / DB], acc_o[c % DB], 0, 0, 0);
       }
@@ -409,7 +416,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
         for (int e = e0; e < e1; ++e) exp_entry(e);
       }
       // row max of S(kt+1), spread over the chunks after its last MFMA
-      if (HAS_NEXT && c >= C_MAX) {
+      if constexpr (C_MAX < NC) if (HAS_NEXT && c >= C_MAX) {
         const int n = NC - C_MAX;
         const int a = ((c - C_MAX) * 32) / n, z = ((c - C_MAX + 1) * 32) / n;
 #pragma unroll
@@ -422,6 +429,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     }
     mx_next = mxn;
     l_run += ls;
+    if (!DEFER) pv_all(p_cur, vslot(kt % kVSlots));
     // keep the copy wait after every MFMA and read of the step
     __builtin_amdgcn_sched_barrier(0);
     wait_copies();
@@ -453,7 +461,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   const BoolC<false> F{};
   if (n_kt == 1) {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, F);
-    pv_all(pf_a, vslot(0));
+    if (DEFER) pv_all(pf_a, vslot(0));
   } else {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, F);
     for (int kt = 1; kt < n_kt - 1; kt += 2) {
@@ -463,10 +471,10 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     const int kl = n_kt - 1;
     if (kl & 1) {
       step(kl, s_b, s_a, pf_b, pf_a, mx_b, mx_a, F, T);
-      pv_all(pf_b, vslot(kl % kVSlots));
+      if (DEFER) pv_all(pf_b, vslot(kl % kVSlots));
     } else {
       step(kl, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, T);
-      pv_all(pf_a, vslot(kl % kVSlots));
+      if (DEFER) pv_all(pf_a, vslot(kl % kVSlots));
     }
   }
 
@@ -768,8 +776,8 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
 
 template <int HD, int NW, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(AttnArgs p) {
-  if constexpr (HD <= 64) flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
-  else flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
+  if constexpr (HD == 128) flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
+  else flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
 }
 template <int HD, int NW>
 int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
@@ -793,8 +801,12 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 // sequences, fewer when S is short so no wave idles on padding rows.
 template <int HD>
 int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
-  if (p.S > 128) return launch_flash<HD, 8>(p, causal, st);
-  if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
+  if constexpr (HD == 256) {  // one wave per SIMD: at most four waves (128 rows)
+    if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
+  } else {
+    if (p.S > 128) return launch_flash<HD, 8>(p, causal, st);
+    if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
+  }
   return launch_flash<HD, 2>(p, causal, st);
 }
 
@@ -804,7 +816,7 @@ int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 using namespace tk;
 
 extern "C" int tk_attention_supported(int64_t head_dim) {
-  return head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128;
+  return head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
 extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_half* v, tk_half* out,
@@ -816,7 +828,7 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
   TK_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && o_strides, TK_ERR_ARG,
              "tk_flash_attn_fwd: null pointer");
   TK_REQUIRE(tk_attention_supported(head_dim), TK_ERR_UNSUPPORTED,
-             "tk_flash_attn_fwd: head_dim=%lld not in {16, 32, 64, 128}", (long long)head_dim);
+             "tk_flash_attn_fwd: head_dim=%lld not in {16, 32, 64, 128, 256}", (long long)head_dim);
   TK_REQUIRE(batch >= 0 && heads >= 0 && seq >= 0 && batch * heads < (1ll << 31) &&
                  seq < (1ll << 30),
              TK_ERR_ARG, "tk_flash_attn_fwd: bad sizes");
@@ -849,6 +861,7 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
     case 16: return dispatch_flash<16>(p, c, st);
     case 32: return dispatch_flash<32>(p, c, st);
     case 64: return dispatch_flash<64>(p, c, st);
-    default: return dispatch_flash<128>(p, c, st);
+    case 128: return dispatch_flash<128>(p, c, st);
+    default: return dispatch_flash<256>(p, c, st);
   }
 }

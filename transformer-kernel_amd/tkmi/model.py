@@ -103,6 +103,18 @@ class _LayerWeights:
     b_2: torch.Tensor
 
 
+# Head dims the attention kernel has tiles for (tk_attention_supported).
+_KERNEL_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+
+def _padded_head_dim(hd: int) -> Optional[int]:
+    """Smallest kernel head dim >= hd, or None above 256."""
+    for k in _KERNEL_HEAD_DIMS:
+        if hd <= k:
+            return k
+    return None
+
+
 class OptimizedTransformer(BaselineTransformer):
     """Drop-in replacement for the harness's ``UserOptimizedTransformer``."""
 
@@ -113,6 +125,10 @@ class OptimizedTransformer(BaselineTransformer):
         self.num_heads = config.num_heads
         self.head_dim = config.d_model // config.num_heads
         self.attn_scale = self.head_dim ** -0.5
+        # Head dims the attention kernel has no tile for run zero-padded to the
+        # next one it has (the reference's kernel pads its head-dim block to a
+        # power of two >= 16, src/kernels.py:268); see _weights().
+        self.head_dim_padded = _padded_head_dim(self.head_dim)
         self._weight_cache: Optional[List[_LayerWeights]] = None
         self._weight_cache_key: Optional[tuple] = None
         self._dense_mask_ref: Optional[weakref.ReferenceType] = None
@@ -138,6 +154,18 @@ class OptimizedTransformer(BaselineTransformer):
             return self._weight_cache
         f16 = lambda t: t.detach().to(torch.float16).contiguous()  # noqa: E731
         f32 = lambda t: t.detach().to(torch.float32).contiguous()  # noqa: E731
+        nh, hd, hp = self.num_heads, self.head_dim, self.head_dim_padded
+
+        def pad_rows(w):  # [H*hd, ...] -> [H*hp, ...], zero rows after each head's hd
+            if hp == hd:
+                return w
+            out = w.new_zeros((nh, hp) + tuple(w.shape[1:]))
+            out[:, :hd] = w.reshape((nh, hd) + tuple(w.shape[1:]))
+            return out.reshape((nh * hp,) + tuple(w.shape[1:]))
+
+        def pad_cols(w):  # [D, H*hd] -> [D, H*hp]
+            return w if hp == hd else pad_rows(w.t()).t()
+
         built = []
         with torch.no_grad():
             for layer in self.layers:
@@ -145,9 +173,11 @@ class OptimizedTransformer(BaselineTransformer):
                 built.append(
                     _LayerWeights(
                         n1_w=f32(layer.norm1.weight), n1_b=f32(layer.norm1.bias), n1_eps=layer.norm1.eps,
-                        w_qkv=f16(torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], 0)),
-                        b_qkv=f32(torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias], 0)),
-                        w_o=f16(at.out_proj.weight), b_o=f32(at.out_proj.bias),
+                        w_qkv=f16(torch.cat([pad_rows(at.q_proj.weight), pad_rows(at.k_proj.weight),
+                                             pad_rows(at.v_proj.weight)], 0)),
+                        b_qkv=f32(torch.cat([pad_rows(at.q_proj.bias), pad_rows(at.k_proj.bias),
+                                             pad_rows(at.v_proj.bias)], 0)),
+                        w_o=f16(pad_cols(at.out_proj.weight)), b_o=f32(at.out_proj.bias),
                         n2_w=f32(layer.norm2.weight), n2_b=f32(layer.norm2.bias), n2_eps=layer.norm2.eps,
                         w_1=f16(layer.ffn_in.weight), b_1=f32(layer.ffn_in.bias),
                         w_2=f16(layer.ffn_out.weight), b_2=f32(layer.ffn_out.bias),
@@ -187,8 +217,8 @@ class OptimizedTransformer(BaselineTransformer):
                 raise ValueError(f"valid_token_mask must be [B, S] = {tuple(x.shape[:2])}, "
                                  f"got {tuple(valid_token_mask.shape)}")
             mask = valid_token_mask.to(device=x.device, dtype=torch.bool).contiguous()
-        if not ops.attention_supported(self.head_dim, torch.float16, x.device):
-            raise NotImplementedError(f"head_dim {self.head_dim} is not supported by the attention kernel")
+        if self.head_dim_padded is None:
+            raise NotImplementedError(f"head_dim {self.head_dim} > 256 has no attention kernel")
         out = self._run_layers(x, mask)
         return out.to(x.dtype)
 
@@ -200,7 +230,8 @@ class OptimizedTransformer(BaselineTransformer):
         and its final-norm output is 0."""
         bsz, seq, d = x.shape
         t = bsz * seq
-        nh, hd = self.num_heads, self.head_dim
+        nh, hd = self.num_heads, self.head_dim_padded
+        dp = nh * hd  # attention width; > d when the head dim is zero-padded
         weights = self._weights()
         fn_w, fn_b, fn_eps = self._final
         dev = x.device
@@ -211,8 +242,8 @@ class OptimizedTransformer(BaselineTransformer):
 
         resid = torch.empty((t, d), dtype=torch.float32, device=dev)
         h = torch.empty((t, d), dtype=torch.float16, device=dev)
-        qkv = torch.empty((t, 3 * d), dtype=torch.float16, device=dev)
-        ctx = torch.empty((t, d), dtype=torch.float16, device=dev)
+        qkv = torch.empty((t, 3 * dp), dtype=torch.float16, device=dev)
+        ctx = torch.empty((t, dp), dtype=torch.float16, device=dev)
         u = torch.empty((t, self.config.ffn_dim), dtype=torch.float16, device=dev)
         out = torch.empty((t, d), dtype=torch.float32, device=dev)
         fuse = (self.settings.fused_norm and d <= self.settings.fused_norm_max_d
@@ -224,7 +255,7 @@ class OptimizedTransformer(BaselineTransformer):
         src = xin  # residual stream input of the next add (the caller's x is never written)
         qkv5 = qkv.view(bsz, seq, 3, nh, hd)
         q, k, v = qkv5.permute(2, 0, 3, 1, 4).unbind(0)  # [B, H, S, hd] strided views
-        ctx3 = ctx.view(bsz, seq, d)
+        ctx3 = ctx.view(bsz, seq, dp)
         last = len(weights) - 1
         for i, lw in enumerate(weights):
             ops.linear(h, lw.w_qkv, lw.b_qkv, out=qkv, name="qkv")
