@@ -629,22 +629,22 @@ int launch_gemm(const GemmArgs& p, hipStream_t st) {
 }
 
 using TileBig = Tile<256, 256, 4, 2, 64, 2>;   // 8 waves of 64 x 128
-using TileWide = Tile<256, 128, 2, 2, 64, 3>;  // 4 waves of 128 x 64, three K stages
 using TileMid = Tile<128, 128, 2, 2, 64, 2>;   // 4 waves of 64 x 64, 2 blocks per CU
 using TileSmall = Tile<64, 64, 1, 1, 64, 2>;   // 1 wave
 
 template <int EPI>
 int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-  const int64_t t256x128 = (int64_t)((p.M + 255) / 256) * ((p.N + 127) / 128);
   const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  // Measured on MI355X (fp16, 256 CUs): 256x256 tiles win once there is at
-  // least one full round of them; narrow outputs (N <= 512) with long K
-  // prefer 256x128 with three K stages, short K the 128x128 tile (two
-  // blocks per CU); 64x64 for the small, launch-bound shapes.
-  if (p.N <= 512 && p.K >= 2048 && t256x128 >= 200) return launch_gemm<TileWide, EPI>(p, st);
-  if (p.N > 512 && t256 >= 256) return launch_gemm<TileBig, EPI>(p, st);
-  if (t128 >= 200) return launch_gemm<TileMid, EPI>(p, st);
+  // Measured on MI355X (fp16, 256 CUs, every epilogue): 256x256 tiles win
+  // when they fill whole rounds of the 256 CUs (or at least two rounds);
+  // with a partial last round (e.g. 384 tiles) the 128x128 tile, two blocks
+  // per CU, is 5-10 % faster, as it is for narrow and short outputs down to
+  // 128 of its tiles; below that the 64x64 tile keeps the CUs busy.  (A
+  // 256x128 three-stage tile never won once the 128x128 tile was taken for
+  // narrow outputs, and is gone.)
+  if (t256 >= 256 && (t256 % 256 == 0 || t256 >= 512)) return launch_gemm<TileBig, EPI>(p, st);
+  if (t128 >= 128) return launch_gemm<TileMid, EPI>(p, st);
   return launch_gemm<TileSmall, EPI>(p, st);
 }
 
