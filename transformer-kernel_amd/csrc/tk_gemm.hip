@@ -362,16 +362,20 @@ __device__ __forceinline__ int epi_off(int row, int chunk) {
   return row * CPR * 16 + ((chunk ^ f) << 4);
 }
 
+// Residual epilogue with per-row validity (padded rows, tk_row_mode): an
+// internal epilogue code, picked when row_valid is given.
+constexpr int kEpiResidRows = 3;
+
 // Each wave stages its WM x WN result tile (in rows of 32 x JC) in its own LDS
 // region, row-major, then reads it back 16 bytes per lane along rows: every
 // global store, and every fp32 residual load, then covers whole 128-byte
 // lines instead of 16-byte pieces of 32 rows.  Bias and GELU are applied in
-// fp32 before the fp16 rounding; the fp32 residual epilogue adds bias and
-// residual on the read-back side.
+// fp32 before the fp16 rounding; the padded-row residual epilogue
+// (kEpiResidRows) adds bias and residual on the read-back side.
 template <class ML, int WAVES_M, int EPI>
 __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                int n0, f16* smem) {
-  constexpr bool F32 = EPI == TK_EPI_BIAS_RESID;
+  constexpr bool F32 = EPI == kEpiResidRows;
   constexpr int ES = F32 ? 4 : 2;
   constexpr int WM = ML::WM, WN = ML::WN, FM = ML::FM, FN = ML::FN, NW = ML::NW;
   constexpr int ROWB = WN * ES;
@@ -476,6 +480,116 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
   }
 }
 
+
+// One pass of the fp32 residual epilogue over accumulator blocks
+// [JB, JB + JC) of a wave:  C[m, n] = resid[m, n] + (acc + bias[n])  (C may
+// alias resid: every element is read and written by the same lane).  The
+// residual rows a lane combines (16 rows of 16 bytes per pass) are loaded
+// in groups of G with one wait per group: all 16 at once, issued before the
+// accumulators are staged in LDS, when the accumulator blocks still live in
+// the pass leave room (at most 64 registers), else 8 after the staging.  In the row-major read-back a lane always
+// lands on the same 16-byte column chunk (64 lanes cover 64 / CPR whole
+// rows), so its bias is one vector.  Launches with padded rows (row_valid)
+// take the kEpiResidRows path of store_tile_lds instead: the per-row
+// validity selects do not fit next to the prefetched rows in 256 registers.
+template <class ML, int WAVES_M, int JB, int JC>
+__device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int mw, int nw,
+                                           char* region) {
+  constexpr int FN = ML::FN;
+  constexpr int CPR = ML::WN * 4 / 16;  // 16-byte chunks per staged row
+  constexpr int RPI = 64 / CPR;         // staged rows per read-back step of the wave
+  constexpr int NIT = JC * 32 / RPI;    // read-back steps of the pass
+  constexpr bool EARLY = FN * (ML::FM - JB) * 16 <= 64;
+  constexpr int G = EARLY ? NIT : NIT / 2;  // rows per load group
+  static_assert(64 % CPR == 0 && (JC * 32) % RPI == 0 && NIT % G == 0, "whole rows per read-back step");
+  const int lane = threadIdx.x & 63;
+  const int ch = lane % CPR, row0 = lane / CPR;
+  const int n = nw + ch * 4;
+  const bool vec = p.vec && n + 3 < p.N;
+  const int mb = mw + JB * 32;  // first row of the pass (wave-uniform)
+  // wave-uniform base + 32-bit lane offsets (a pass spans 32 rows)
+  const float* rbase = p.resid + (int64_t)mb * p.ldr + nw;
+  const uint32_t ldr = (uint32_t)p.ldr;
+
+  f32x4 r[G];
+  auto fetch = [&](int g) {
+#pragma unroll
+    for (int it = 0; it < G; ++it) {
+      const int row = (g * G + it) * RPI + row0;
+      r[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (vec && mb + row < p.M) r[it] = *reinterpret_cast<const f32x4*>(rbase + ((uint32_t)row * ldr + ch * 4));
+    }
+  };
+  auto combine = [&](int g, const f32x4& b) {
+#pragma unroll
+    for (int it = 0; it < G; ++it) {
+      const int row = (g * G + it) * RPI + row0;
+      const int m = mb + row;
+      if (m < p.M && n < p.N) {
+        const f32x4 d = *reinterpret_cast<const f32x4*>(region + epi_off<CPR>(row, ch));
+        float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
+        if (vec) {
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = r[it][e] + (d[e] + b[e]);
+          *reinterpret_cast<f32x4*>(cr) = o;
+        } else {
+          const float* rr = p.resid + (int64_t)m * p.ldr + n;
+          for (int e = 0; e < 4 && n + e < p.N; ++e)
+            cr[e] = rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f));
+        }
+      }
+    }
+  };
+
+  f32x4 b = {0.f, 0.f, 0.f, 0.f};
+  if (p.bias && vec) {
+    if (p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
+    else b = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
+  }
+  if constexpr (EARLY) fetch(0);
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = i * 32 + 8 * q + 4 * (lane >> 5);  // 4 consecutive n of this lane
+#pragma unroll
+      for (int jj = 0; jj < JC; ++jj) {
+        const f32x16& a = acc[i][JB + jj];
+        *reinterpret_cast<f32x4*>(region + epi_off<CPR>(jj * 32 + (lane & 31), nl / 4)) =
+            f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+      }
+    }
+  asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
+  if constexpr (!EARLY) fetch(0);
+  combine(0, b);
+#pragma unroll
+  for (int g = 1; g < NIT / G; ++g) {
+    fetch(g);
+    combine(g, b);
+  }
+  asm volatile("" ::: "memory");
+}
+
+// fp32 residual epilogue: one resid_pass per group of JC accumulator blocks
+// (two groups when the staging region holds one 32-row block per wave).
+template <class ML, int WAVES_M>
+__device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
+                                                 int n0, f16* smem) {
+  constexpr int FM = ML::FM, NW = ML::NW;
+  constexpr int ROWB = ML::WN * 4;
+  constexpr int LDS_BYTES = ML::LDS_HALVES * 2;
+  constexpr int JC = (NW * FM * 32 * ROWB <= LDS_BYTES) ? FM : (NW * 32 * ROWB <= LDS_BYTES ? 1 : 0);
+  static_assert(JC > 0 && FM % JC == 0 && FM / JC <= 2, "staging region does not fit");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mw = m0 + (wave % WAVES_M) * ML::WM;
+  const int nw = n0 + (wave / WAVES_M) * ML::WN;
+  char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
+  __syncthreads();  // every wave is done with the main-loop buffers
+  resid_pass<ML, WAVES_M, 0, JC>(p, acc, mw, nw, region);
+  if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC>(p, acc, mw, nw, region);
+}
+
 template <class T, int EPI, bool DIRECT>
 __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   constexpr int BM = T::BM, BN = T::BN;
@@ -487,7 +601,10 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   f32x16 acc[ML::FN][ML::FM];
   ML::run(p, tm * BM, tn * BN, smem, acc);
-  store_tile_lds<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem);
+  if constexpr (EPI == TK_EPI_BIAS_RESID)
+    store_tile_resid<ML, T::WAVES_M>(p, acc, tm * BM, tn * BN, smem);
+  else
+    store_tile_lds<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem);
 }
 
 // Full-row variant: BN == N, so each block owns complete output rows and
@@ -710,7 +827,8 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
   switch (epilogue) {
     case TK_EPI_BIAS: return gemm_dispatch<TK_EPI_BIAS>(p, st);
     case TK_EPI_BIAS_GELU: return gemm_dispatch<TK_EPI_BIAS_GELU>(p, st);
-    default: return gemm_dispatch<TK_EPI_BIAS_RESID>(p, st);
+    default:
+      return p.row_valid ? gemm_dispatch<kEpiResidRows>(p, st) : gemm_dispatch<TK_EPI_BIAS_RESID>(p, st);
   }
 }
 
