@@ -62,20 +62,20 @@ __device__ __forceinline__ float group_max(float v) {
 // approximation): for z >= 0
 //   erfc(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 //   t = 1 / (1 + p z),  |erf error| <= 1.5e-7.
-// With z = |x|/sqrt(2) and q = 0.5*x*erfc(z):  GELU(x) = x - q for x >= 0 and
-// q for x < 0 (no 1+erf cancellation), so |GELU error| <= 0.75e-7 * |x|.
-// ~14 VALU ops (one rcp, one exp2) instead of a general-purpose erff.
+// With z = |x|/sqrt(2) and r = 0.5*|x|*erfc(z) >= 0, GELU(x) = max(x, 0) - r
+// for either sign of x (x - x*Phi(-x) for x >= 0, x*Phi(x) = -r for x < 0),
+// with no 1+erf cancellation, so |GELU error| <= 0.75e-7 * |x|.  The 1/sqrt(2)
+// is folded into p and the exponent, the 0.5 into the coefficients: 14 VALU
+// ops (one rcp, one exp2), no select.
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float a = fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  poly *= t;
-  const float e = __builtin_amdgcn_exp2f(-a * a * 1.4426950408889634f);  // exp(-z^2)
-  const float q = 0.5f * x * poly * e;
-  return x >= 0.f ? x - q : q;
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752440f, ax, 1.0f));
+  float poly = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  poly = fmaf(poly, t, 0.5f * 1.421413741f);
+  poly = fmaf(poly, t, 0.5f * -0.284496736f);
+  poly = fmaf(poly, t, 0.5f * 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634f));  // exp(-z^2)
+  return fmaf(-(ax * t) * poly, e, fmaxf(x, 0.0f));
 }
 
 }  // namespace tk
