@@ -43,7 +43,6 @@ namespace {
 constexpr int kBN = 64;     // keys per tile
 constexpr int kKSlots = 2;  // flash_dma_body K tiles in LDS: t+1 (read), t+2 (landing)
 
-typedef __attribute__((address_space(3))) char lds_char;
 typedef __fp16 hf16x2 __attribute__((ext_vector_type(2)));  // operand type of the fdot2 builtin
 typedef __fp16 tr_f16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) tr_f16x4 lds_tr_f16x4;
@@ -88,24 +87,6 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 // s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding).
 __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
-
-// One 16-byte-per-lane global -> LDS copy of a wave (lane l lands at
-// lds_addr + 16*l).  Issued as inline assembly so that the compiler's wait
-// insertion, which cannot tell the ring slots apart, does not put a vmcnt(0)
-// in front of every later LDS read; the kernel waits for its copies itself
-// (wait_copies before each workgroup barrier).  M0 is saved and restored.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(gptr), "s"(lds_addr)
-      : "memory");
-}
 
 template <bool B>
 struct BoolC {

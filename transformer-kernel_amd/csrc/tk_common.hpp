@@ -21,6 +21,27 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+typedef __attribute__((address_space(3))) char lds_char;
+
+// One 16-byte-per-lane global -> LDS copy of a wave (global_load_lds_dwordx4:
+// lane l's 16 bytes land at lds_addr + 16*l; lds_addr wave-uniform).  Issued
+// as inline assembly so that the compiler's wait insertion, which cannot tell
+// a kernel's LDS ring slots apart, does not put a vmcnt wait in front of
+// every later LDS read; the kernels wait for their copies themselves (vmcnt
+// before each workgroup barrier).  M0 is saved and restored.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds_addr)
+      : "memory");
+}
+
 // ---------------------------------------------------------------- errors --
 // Per-thread status text behind tk_last_error_string().
 void set_error(const char* fmt, ...);

@@ -159,11 +159,13 @@ struct Mainloop {
 
   __device__ static void run_direct(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave % WAVES_M;
     const int wn = wave / WAVES_M;
     f16* As = smem;                      // [STAGES][BM][BK]
     f16* Ws = smem + STAGES * BM * BK;   // [STAGES][BN][BK]
+    const uint32_t lds_a = (uint32_t)(size_t)(lds_char*)As;
+    const uint32_t lds_w = (uint32_t)(size_t)(lds_char*)Ws;
     const int nk = p.K / BK;
 
     const f16* ga[A_INSTS];
@@ -180,38 +182,38 @@ struct Mainloop {
       const int c = swz<BK>(r, lane % CPR) - r * BK;
       gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
     }
-    auto issue = [&](int kt, int stage) {  // start tile kt's copy into `stage`
-      f16* a_s = As + stage * BM * BK;
-      f16* w_s = Ws + stage * BN * BK;
-#pragma unroll
-      for (int i = 0; i < A_INSTS; ++i)
-        __builtin_amdgcn_global_load_lds(ga[i] + kt * BK, (lds_void*)(a_s + (wave * A_INSTS + i) * RPC * BK),
-                                         16, 0, 0);
-#pragma unroll
-      for (int i = 0; i < W_INSTS; ++i)
-        __builtin_amdgcn_global_load_lds(gw[i] + kt * BK, (lds_void*)(w_s + (wave * W_INSTS + i) * RPC * BK),
-                                         16, 0, 0);
+    // Wave copy c of tile kt into `stage`: copies 0..A_INSTS-1 are A rows,
+    // the rest W rows, 1 KB each.
+    auto copy = [&](int kt, int stage, int c) {
+      if (c < A_INSTS)
+        dma16(ga[c] + kt * BK, lds_a + 2 * (stage * BM * BK + (wave * A_INSTS + c) * RPC * BK));
+      else
+        dma16(gw[c - A_INSTS] + kt * BK,
+              lds_w + 2 * (stage * BN * BK + (wave * W_INSTS + c - A_INSTS) * RPC * BK));
     };
     const int frow = lane & 31;   // fragment row within a 32-row block
     const int fhalf = lane >> 5;  // which 8-wide k half of a 16-wide k step
     f16x8 fa[2][FM], fw[2][FN];
-    auto read = [&](int b, int stage, int kk) {
-      const f16* a_s = As + stage * BM * BK;
-      const f16* w_s = Ws + stage * BN * BK;
+    // Fragment r of k-step kk: r < FM reads A block r, else W block r - FM.
+    auto read1 = [&](int b, int stage, int kk, int r) {
       const int ch = 2 * kk + fhalf;
+      if (r < FM)
+        fa[b][r] = *reinterpret_cast<const f16x8*>(As + stage * BM * BK + swz<BK>(wm * WM + r * 32 + frow, ch));
+      else
+        fw[b][r - FM] =
+            *reinterpret_cast<const f16x8*>(Ws + stage * BN * BK + swz<BK>(wn * WN + (r - FM) * 32 + frow, ch));
+    };
+    auto read = [&](int b, int stage, int kk) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j)
-        fa[b][j] = *reinterpret_cast<const f16x8*>(a_s + swz<BK>(wm * WM + j * 32 + frow, ch));
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-        fw[b][i] = *reinterpret_cast<const f16x8*>(w_s + swz<BK>(wn * WN + i * 32 + frow, ch));
+      for (int r = 0; r < FM + FN; ++r) read1(b, stage, kk, r);
+    };
+    auto mma1 = [&](int b, int x) {  // MFMA x of a k-step: W block x / FM, A block x % FM
+      const int i = x / FM, j = x % FM;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
     };
     auto mma = [&](int b) {
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+      for (int x = 0; x < FM * FN; ++x) mma1(b, x);
     };
     // Scheduling hint for one k-step: one fragment read after each of the
     // first FM + FN MFMAs, then the remaining MFMAs.
@@ -226,7 +228,10 @@ struct Mainloop {
 
 #pragma unroll
     for (int s = 0; s < STAGES; ++s)
-      if (s < nk) issue(s, s);
+      if (s < nk) {
+#pragma unroll
+        for (int c = 0; c < INSTS; ++c) copy(s, s, c);
+      }
     if (nk >= STAGES) wait_vmcnt<(STAGES - 1) * INSTS>();
     else wait_vmcnt<0>();
     lds_barrier();
@@ -244,7 +249,10 @@ struct Mainloop {
         if (kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * INSTS>();
         else wait_vmcnt<0>();
         lds_barrier();
-        if (kt + STAGES < nk) issue(kt + STAGES, cur);
+        if (kt + STAGES < nk) {
+#pragma unroll
+          for (int c = 0; c < INSTS; ++c) copy(kt + STAGES, cur, c);
+        }
         cur = cur + 1 == STAGES ? 0 : cur + 1;
         read(0, cur, 0);
       }
