@@ -755,11 +755,186 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   }
 }
 
+// ---- one key tile (S <= 64, head_dim <= 64) ----
+// Short sequences are latency-bound (the reference's B256 S64 config runs
+// 2048 heads of one tile each): a workgroup loads Q, one K and one V tile
+// and writes O once.  This body keeps only what one tile needs -- no
+// next-tile scores, no deferred P, no copy ring -- so it needs about a third
+// of flash_dma_body's registers and 16 KB of LDS, and all workgroups of such
+// a launch are resident at once.  For one tile the DMA body's running max is
+// the tile max, so the operand layouts, the exponentials, the fp16 row sums
+// and the MFMA order here are the same and the results are identical.
 template <int HD, int NW, bool CAUSAL, bool KMASK>
-__global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(AttnArgs p) {
+__device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
+  constexpr int BM = 32 * NW;
+  constexpr int RB = HD * 2;               // K / V tile row bytes
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;           // bytes per K or V tile
+  constexpr int COPIES = TILE / 1024;      // 1 KB wave copies per tile
+  constexpr int CPW = (COPIES + NW - 1) / NW;
+  constexpr int RPC = 1024 / RB;           // tile rows per copy
+  constexpr int DB = (HD + 31) / 32;       // 32-row blocks of the O^T accumulator
+  constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
+  constexpr int NS = 2 * KSTEPS;           // S^T MFMAs
+  constexpr int NP = 4 * DB;               // O^T MFMAs
+  static_assert(HD <= 64 && BM >= kBN, "one key tile, every query row in the workgroup");
+  static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
+
+  __shared__ __attribute__((aligned(16))) char smem[2 * TILE];
+  const uint32_t lds_base = (uint32_t)(size_t)(lds_char*)smem;
+  const char* ks_ = smem;
+  const char* vs_ = smem + TILE;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bh = blockIdx.x;  // one workgroup per (batch, head): S <= BM
+  const int b = bh / p.H, h = bh % p.H;
+  const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
+  const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
+  const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const int my_row = wave * 32 + (lane & 31);
+  const int g = lane >> 5;
+
+  // K and V tiles, row-major as in flash_dma_body (K chunk-swizzled, V with
+  // the transposed-read swizzle); rows past S re-read row S-1 (finite,
+  // masked or multiplied by P = 0).
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int ci = wave + i * NW;
+    if (COPIES % NW == 0 || ci < COPIES) {
+      const int row = ci * RPC + lane / CPR;
+      const int phys = lane % CPR;
+      const int key = min(row, p.S - 1);
+      const int kc = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
+      const int vc = (phys ^ vswz<RB>(row)) * 8;
+      dma16(kb + (int64_t)key * p.ks[2] + kc, lds_base + ci * 1024);
+      dma16(vb + (int64_t)key * p.vs[2] + vc, lds_base + TILE + ci * 1024);
+    }
+  }
+  // Q^T fragments (B operand): lane supplies Q[row][16*kk + 8*g .. +8].
+  f16x8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if (my_row < p.S)
+      qf[kk] = *reinterpret_cast<const f16x8*>(qb + (int64_t)my_row * p.qs[2] + kk * 16 + g * 8);
+    else
+      qf[kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  // bit j: key j is valid
+  const uint64_t kbits = KMASK ? (uint64_t)__ballot(p.kv[b * p.kvs + min(lane, p.S - 1)] != 0) : 0ull;
+  wait_copies();
+  __syncthreads();
+
+  // ---- S^T = K . Q^T: entry r of block kb2 is key 32*kb2 + 8*(r/4) + 4*g + r%4 ----
+  f32x16 s[2];
+#pragma unroll
+  for (int c = 0; c < NS; ++c) {
+    const int kb2 = c / KSTEPS, kk = c % KSTEPS;
+    const f16x8 kf = *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>(kb2 * 32 + (lane & 31), 2 * kk + g));
+    s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], kk == 0 ? f32x16{} : s[kb2], 0, 0, 0);
+  }
+  float mx = -INFINITY;
+  const uint64_t kb64 = kbits >> (4 * g);
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+      const int key = j + 4 * g;
+      if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kb64 >> j) & 1) == 0)) s[kb2][r] = -INFINITY;
+      mx = fmaxf(mx, s[kb2][r]);
+    }
+  mx = pair_max(mx);
+  const float cs = p.scale_log2;
+  const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
+  const float m_use = m_tile == -INFINITY ? 0.f : m_tile;
+
+  // ---- P in fp16 (8 consecutive entries = one B operand) and its row sum ----
+  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
+  f16x8 pf[4];
+  float ls = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; e += 2) {
+    const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use)),
+                      (f16)__builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use))};
+    pf[e >> 3][e & 7] = hp[0];
+    pf[e >> 3][(e & 7) + 1] = hp[1];
+    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+  }
+
+  // ---- O^T = V^T . P^T; V^T operands by transposed LDS reads (see flash_dma_body) ----
+  int v_rd[2][DB];
+  {
+    const int tq = lane >> 4, ts = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
+        const int col = 32 * d + (HD >= 32 ? 16 * (tq & 1) : 0) + 4 * (ts & 3);  // HD 16: lanes >= 16 are zeroed
+        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
+      }
+  }
+  const bool d_ok = HD % 32 == 0 || (lane & 31) < HD;
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int c = 0; c < NP; ++c) {
+    const int t = c / DB, d = c % DB;
+    const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
+    const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
+    const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
+    f16x8 vf = __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2, 3, 4,
+                                       5, 6, 7);
+    if (!d_ok) vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    acc_o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], t == 0 ? f32x16{} : acc_o[d], 0, 0, 0);
+  }
+
+  // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
+  const float inv = 1.0f / pair_sum(ls);
+  if (my_row < p.S) {
+    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int dd = d * 32 + 8 * q + 4 * g;
+        if (dd < HD) {
+          f16x4 t = {(f16)(acc_o[d][4 * q] * inv), (f16)(acc_o[d][4 * q + 1] * inv),
+                     (f16)(acc_o[d][4 * q + 2] * inv), (f16)(acc_o[d][4 * q + 3] * inv)};
+          *reinterpret_cast<f16x4*>(ob + dd) = t;
+        }
+      }
+  }
+}
+
+// Short sequences (NW <= 4) at head_dim <= 32 ask for two waves per SIMD:
+// left alone the compiler spends 280-300 registers on them (one wave per
+// SIMD), and these launches are latency-bound (b256 s64 d32: 14.4 -> 12.4
+// us).  At head_dim 64 the same bound spills, so it is not applied there.
+template <int HD, int NW, bool CAUSAL, bool KMASK>
+__global__ __launch_bounds__(NW * 64, (NW <= 4 && HD <= 32) ? 2 : 1) void flash_fwd_kernel(AttnArgs p) {
   if constexpr (HD == 128) flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
   else flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
 }
+template <int HD, int NW, bool CAUSAL, bool KMASK>
+__global__ __launch_bounds__(NW * 64, 4) void flash_single_kernel(AttnArgs p) {
+  flash_single_body<HD, NW, CAUSAL, KMASK>(p);
+}
+template <int HD>
+int launch_single(const AttnArgs& p, bool causal, hipStream_t st) {
+  const dim3 g((unsigned)(p.B * p.H)), blk(2 * 64);
+  const bool km = p.kv != nullptr;
+  if (causal && km)
+    hipLaunchKernelGGL((flash_single_kernel<HD, 2, true, true>), g, blk, 0, st, p);
+  else if (causal)
+    hipLaunchKernelGGL((flash_single_kernel<HD, 2, true, false>), g, blk, 0, st, p);
+  else if (km)
+    hipLaunchKernelGGL((flash_single_kernel<HD, 2, false, true>), g, blk, 0, st, p);
+  else
+    hipLaunchKernelGGL((flash_single_kernel<HD, 2, false, false>), g, blk, 0, st, p);
+  return check_launch("tk_flash_attn_fwd");
+}
+
 template <int HD, int NW>
 int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   constexpr int BM = 32 * NW;
@@ -779,7 +954,8 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 }
 
 // Query rows per workgroup: 256 (8 waves sharing each K/V tile) for long
-// sequences, fewer when S is short so no wave idles on padding rows.
+// sequences, fewer when S is short so no wave idles on padding rows; one key
+// tile (S <= 64) at head_dim <= 64 takes flash_single_body.
 template <int HD>
 int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   if constexpr (HD == 256) {  // one wave per SIMD: at most four waves (128 rows)
@@ -788,7 +964,8 @@ int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
     if (p.S > 128) return launch_flash<HD, 8>(p, causal, st);
     if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   }
-  return launch_flash<HD, 2>(p, causal, st);
+  if constexpr (HD <= 64) return launch_single<HD>(p, causal, st);
+  else return launch_flash<HD, 2>(p, causal, st);
 }
 
 }  // namespace
