@@ -172,8 +172,10 @@ def test_flash_rejects_short_key_mask_stride_without_gpu():
 
 
 # Attention instantiations the five benchmark configs dispatch:
-# (head_dim, waves per workgroup, causal) -- C1, C2, C3/C5, C4.
-BENCH_ATTENTION = [(32, 4, 1), (64, 2, 0), (64, 8, 1), (128, 8, 1)]
+# (kernel, head_dim, waves per workgroup, causal) -- C1, C2 (one key tile),
+# C3/C5, C4.
+BENCH_ATTENTION = [("flash_fwd_kernel", 32, 4, 1), ("flash_single_kernel", 64, 2, 0), ("flash_fwd_kernel", 64, 8, 1),
+                   ("flash_fwd_kernel", 128, 8, 1)]
 
 
 def test_hot_kernels_use_no_scratch():
@@ -187,8 +189,8 @@ def test_hot_kernels_use_no_scratch():
     usage = json.loads(tkbuild.RESOURCE_PATH.read_text())
     hot = [k for k in usage if any(s in k for s in ("gemm_kernel", "gemm_ln_kernel", "ln_rows_kernel", "softmax_"))]
     assert len(hot) >= 30
-    for hd, nw, causal in BENCH_ATTENTION:
-        hot.append(f"_ZN2tk12_GLOBAL__N_116flash_fwd_kernelILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
+    for name, hd, nw, causal in BENCH_ATTENTION:
+        hot.append(f"_ZN2tk12_GLOBAL__N_1{len(name)}{name}ILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
     missing = [k for k in hot if k not in usage]
     assert not missing, missing
     spilled = {k: usage[k]["scratch"] for k in hot if usage[k].get("scratch", 0) > 0}
