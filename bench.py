@@ -88,6 +88,8 @@ def kernel_units(name: str, cfg) -> tuple:
     if name in gemm:
         return gemm[name], "flop", "mfma"
     if name == "flash_attn":
+        if s <= 64:  # one key tile per head: Q, K, V read and O written once (fp16)
+            return 8.0 * t * d, "byte", "hbm"
         pairs = s * (s + 1) / 2 if causal else s * s
         return 4.0 * b * d * pairs, "flop", "mfma"
     ln_bytes = {"ln_in": 6, "ln2": 6, "ln_next": 6, "ln_final": 8}
