@@ -262,6 +262,7 @@ struct Mainloop {
       cur = cur + 1 == STAGES ? 0 : cur + 1;
       read(0, cur, 0);
       mma(1);
+      interleave();  // the fresh reads go out between the MFMAs, not after them
     }
     if (nk > 0) {  // K = 0: no tile, the product is 0
       ksteps();
