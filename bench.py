@@ -87,6 +87,10 @@ def kernel_units(name: str, cfg) -> tuple:
     }
     if name in gemm:
         return gemm[name], "flop", "mfma"
+    if name == "small_forward":  # the whole forward (every layer) in one launch
+        pairs = s * (s + 1) / 2 if causal else s * s
+        per_layer = 2.0 * t * (3 * d * d + d * d + 2 * d * f) + 4.0 * b * d * pairs
+        return per_layer * cfg[5], "flop", "mfma"
     if name == "flash_attn":
         if s <= 64:  # one key tile per head: Q, K, V read and O written once (fp16)
             return 8.0 * t * d, "byte", "hbm"

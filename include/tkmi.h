@@ -173,6 +173,46 @@ int tk_masked_softmax(const float *scores, tk_half *probs, int64_t groups,
                       int64_t seq, int causal, const int32_t *key_len,
                       int64_t heads_per_batch, void *stream);
 
+/*
+ * The whole dense forward of a narrow model in one launch: for each of the
+ * batch's sequences, every layer of
+ *   h = LN1(x); qkv = h.W_qkv^T + b; ctx = attention(q, k, v);
+ *   x += ctx.W_o^T + b_o; h = LN2(x); u = gelu(h.W_1^T + b_1);
+ *   x += u.W_2^T + b_2
+ * then out = LN_final(x), with the numerics of the layer-by-layer path
+ * (fp16 operands, fp32 accumulation, residual and statistics).
+ * x, out: [batch, seq, d_model] f32 (out may not alias x).
+ * Weights stacked over the layers, each layer's block as the layer-by-layer
+ * calls take it: w_qkv [L][3*heads*hd][d] f16 (head rows zero-padded to hd =
+ * head_dim_padded), b_qkv [L][3*heads*hd] f32, w_o [L][d][heads*hd] f16,
+ * b_o [L][d], w_1 [L][ffn][d] f16, b_1 [L][ffn], w_2 [L][d][ffn] f16,
+ * b_2 [L][d], n1_w, n1_b, n2_w, n2_b [L][d] f32, nf_w, nf_b [d] f32; all
+ * 16-byte aligned.
+ * scale: the attention scale (1/sqrt(unpadded head_dim)).  Dense inputs only
+ * (no padding mask).  Shapes: tk_small_forward_supported.
+ * Replaces the layer loop of OptimizedTransformer._run_layers_fused
+ * (src/optimized.py:488-554) for the narrow configs (reference config 1 and
+ * the appendix cases of src/configs/shapes.json with d_model 128).
+ */
+int tk_small_forward(const float *x, float *out, int64_t batch, int64_t seq,
+                     int64_t d_model, int64_t heads, int64_t head_dim_padded,
+                     int64_t ffn_dim, int64_t layers, int causal,
+                     const tk_half *w_qkv, const float *b_qkv,
+                     const tk_half *w_o, const float *b_o,
+                     const tk_half *w_1, const float *b_1,
+                     const tk_half *w_2, const float *b_2,
+                     const float *n1_w, const float *n1_b,
+                     const float *n2_w, const float *n2_b,
+                     const float *nf_w, const float *nf_b, float n1_eps,
+                     float n2_eps, float nf_eps, float scale, void *stream);
+
+/* 1 when tk_small_forward takes the shape (seq <= 128, d_model = ffn_dim =
+ * 128, heads * head_dim_padded = 128, head_dim_padded in {16, 32, 64, 128}),
+ * else 0.  No counterpart in the reference (its narrow configs run the
+ * layer loop). */
+int tk_small_forward_supported(int64_t seq, int64_t d_model, int64_t heads,
+                               int64_t head_dim_padded, int64_t ffn_dim);
+
 #ifdef __cplusplus
 }
 #endif

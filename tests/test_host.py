@@ -128,6 +128,12 @@ def test_capability_probes():
     lib = _lib.load()
     assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256, 512)] == [0, 1, 1, 1, 1, 1, 0]
     assert [lib.tk_gemm_ln_supported(n) for n in (64, 128, 256, 512, 1024)] == [0, 1, 1, 1, 0]
+    # whole-forward kernel: S <= 128, d_model = ffn = 128, heads * padded head_dim = 128
+    small = lib.tk_small_forward_supported
+    assert [small(s, 128, 4, 32, 128) for s in (0, 1, 77, 128, 129)] == [0, 1, 1, 1, 0]
+    assert [small(128, 128, h, 128 // h, 128) for h in (1, 2, 4, 8)] == [1, 1, 1, 1]
+    assert small(128, 128, 16, 16, 128) == 0  # head_dim 8 pads to 16: attention width 256
+    assert small(128, 256, 4, 64, 128) == 0 and small(128, 128, 4, 32, 256) == 0
 
 
 @pytest.mark.parametrize(
@@ -146,6 +152,12 @@ def test_capability_probes():
         ("tk_gemm_bias_add_ln", (16, 16, 16, 16, None, 16, 16, 16, None, 16, 1, 4, 128, 16, 1e-5, 16, 0, None),
          _lib.TK_ERR_ARG),
         ("tk_masked_softmax", (None, None, 1, 4, 1, None, 1, None), _lib.TK_ERR_ARG),
+        ("tk_small_forward", (None, 16) + (1, 128, 128, 4, 32, 128, 4, 1) + (16,) * 14 + (1e-5, 1e-5, 1e-5, 0.17, None),
+         _lib.TK_ERR_ARG),
+        ("tk_small_forward", (16, 16) + (1, 256, 128, 4, 32, 128, 4, 1) + (16,) * 14 + (1e-5, 1e-5, 1e-5, 0.17, None),
+         _lib.TK_ERR_UNSUPPORTED),
+        ("tk_small_forward", (16, 16) + (1, 128, 128, 4, 32, 128, 0, 1) + (16,) * 14 + (1e-5, 1e-5, 1e-5, 0.17, None),
+         _lib.TK_ERR_ARG),
     ],
 )
 def test_argument_validation_without_gpu(fn, args, code):

@@ -43,9 +43,6 @@ namespace {
 constexpr int kBN = 64;     // keys per tile
 constexpr int kKSlots = 2;  // flash_dma_body K tiles in LDS: t+1 (read), t+2 (landing)
 
-typedef __fp16 hf16x2 __attribute__((ext_vector_type(2)));  // operand type of the fdot2 builtin
-typedef __fp16 tr_f16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) tr_f16x4 lds_tr_f16x4;
 
 // LDS byte offset of the 16-byte chunk `chunk` of row `row` in a K tile
 // whose rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane
@@ -71,19 +68,6 @@ __device__ __forceinline__ int vswz(int row) {
   else return 0;
 }
 
-// Max / sum over the lane pair (l, l^32) that holds one query row.
-// v_permlane32_swap of a register with itself leaves, in every lane, its own
-// value in one half of the result and the partner's in the other, so a
-// symmetric op over both halves is the pair reduction -- two VALU ops, no
-// LDS round trip.
-__device__ __forceinline__ float pair_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding).
 __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }

@@ -22,6 +22,24 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 
 typedef __attribute__((address_space(3))) char lds_char;
+typedef __fp16 hf16x2 __attribute__((ext_vector_type(2)));  // operand type of the fdot2 builtin
+typedef __fp16 tr_f16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) tr_f16x4 lds_tr_f16x4;
+
+// Max / sum over the lane pair (l, l^32) that holds one row of a 32x32 MFMA
+// accumulator (lanes l and l^32 hold the two halves of column l & 31).
+// v_permlane32_swap of a register with itself leaves, in every lane, its own
+// value in one half of the result and the partner's in the other, so a
+// symmetric op over both halves is the pair reduction -- two VALU ops, no
+// LDS round trip.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // One 16-byte-per-lane global -> LDS copy of a wave (global_load_lds_dwordx4:
 // lane l's 16 bytes land at lds_addr + 16*l; lds_addr wave-uniform).  Issued

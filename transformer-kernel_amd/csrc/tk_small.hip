@@ -1,0 +1,520 @@
+// Whole-forward kernel for narrow models (d_model = ffn_dim = 128, attention
+// width 128, S <= 128): the reference's own config 1 and most of its
+// appendix shapes, where the layer-by-layer path is ~36 launches of a few
+// microseconds each per forward.
+//
+// One workgroup (4 waves) runs the complete forward of one sequence, all
+// layers, without touching HBM between kernels:
+//   * the fp32 residual stream x stays in registers for the whole forward:
+//     wave w owns columns [32w, 32w+32) of every row, in the 32x32 MFMA
+//     accumulator layout of C^T (lane l holds 4 consecutive columns of row
+//     32*mb + (l & 31) per 4 registers), so the out-projection and FFN-down
+//     products accumulate straight into it;
+//   * LayerNorm row statistics are combined across the 4 waves through a
+//     small LDS table (exact two-pass mean / variance);
+//   * the GEMMs compute C^T = W . A^T on v_mfma_f32_32x32x16_f16: the A
+//     operand is a weight fragment (16 bytes per lane, read from L2 one phase
+//     ahead of its use), the B operand an activation fragment from a
+//     chunk-swizzled LDS tile (h, Q, K, ctx, u);
+//   * attention: S^T = K . Q^T per 32-row query block over at most 4 key
+//     blocks, fp32 scores, -inf masking, exact row max, exp2 with the scale
+//     folded, fp16 P, row sums of the fp16 P, O^T = V^T . P^T with V^T from
+//     ds_read_b64_tr_b16 reads of the row-major V tile.
+// Numerics are those of the layer-by-layer path (src/optimized.py:488-554;
+// src/kernels.py:112-134): fp16 operands, fp32 accumulation, residual and
+// statistics, bias/GELU/residual in fp32 before each fp16 rounding.
+#include "tk_common.hpp"
+
+namespace tk {
+namespace {
+
+constexpr int kMaxRows = 128;  // S <= 128: four 32-row blocks
+constexpr int kPitch = 256;    // bytes per LDS tile row (128 fp16 columns)
+constexpr int kTile = kMaxRows * kPitch;
+
+struct SmallArgs {
+  const float* x;
+  float* out;
+  const f16* w_qkv;  // [L][3*DP][D]
+  const float* b_qkv;
+  const f16* w_o;  // [L][D][DP]
+  const float* b_o;
+  const f16* w_1;  // [L][F][D]
+  const float* b_1;
+  const f16* w_2;  // [L][D][F]
+  const float* b_2;
+  const float* n1_w;  // [L][D]
+  const float* n1_b;
+  const float* n2_w;
+  const float* n2_b;
+  const float* nf_w;  // [D]
+  const float* nf_b;
+  float n1_eps, n2_eps, nf_eps;
+  float scale_log2;  // attention scale * log2(e)
+  int S, L, H;
+};
+
+// Byte offset of 16-byte chunk c of row r in an activation tile: the chunk
+// index is XOR-ed with r mod 16, so the 32 rows of a fragment read (one
+// chunk each) and the row writes hit distinct banks.
+__device__ __forceinline__ int act_off(int r, int c) { return r * kPitch + ((c ^ (r & 15)) << 4); }
+// V tile: chunk XOR 4*(r mod 4), the layout the transposed reads need (the
+// four rows a 16-lane group reads put their bytes on distinct banks).
+__device__ __forceinline__ int v_off(int r, int c) { return r * kPitch + ((c ^ (4 * (r & 3))) << 4); }
+
+// Workgroup barrier for LDS hand-offs: this wave's LDS accesses complete
+// (lgkmcnt 0), then s_barrier.  __syncthreads() would also wait for every
+// outstanding global load -- the weight fragments issued a phase ahead.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int D, int DP, int F, int HDP, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
+  static_assert(D == 128 && DP == 128 && F == 128, "one width: 4 waves x 32 columns");
+  static_assert(HDP == 16 || HDP == 32 || HDP == 64 || HDP == 128, "head dims with an MFMA k-step");
+  constexpr int KD = D / 16, KP = DP / 16, KF = F / 16;  // k-steps
+  constexpr int NQ = 3 * DP / 32 / 4;                      // QKV n-blocks per wave
+  constexpr int HK = HDP / 16;                             // k-steps of one head
+  constexpr int DB = (HDP + 31) / 32;                      // 32-row blocks of O^T
+
+  // Per-layer vectors, staged in LDS one layer ahead (double-buffered):
+  // b_qkv | b_o | b_1 | b_2 | n1_w | n1_b | n2_w | n2_b, then the final norm.
+  constexpr int V_BO = 3 * DP, V_B1 = V_BO + D, V_B2 = V_B1 + F, V_N1W = V_B2 + D, V_N1B = V_N1W + D,
+                V_N2W = V_N1B + D, V_N2B = V_N2W + D, VEC = V_N2B + D;
+  constexpr int VPT = VEC / 256;  // vector floats per thread
+  static_assert(VEC % 256 == 0, "whole vector rows per thread");
+
+  __shared__ __attribute__((aligned(16))) char smem[4 * kTile + 2 * 4 * kMaxRows * 4 + (2 * VEC + 2 * D) * 4];
+  char* Ht = smem;                // h (LayerNorm output) / ctx
+  char* Qt = smem + kTile;        // Q / u
+  char* Kt = smem + 2 * kTile;    // K
+  char* Vt = smem + 3 * kTile;    // V
+  float* stats = reinterpret_cast<float*>(smem + 4 * kTile);  // [2][4 waves][128 rows]
+  float* vecs = stats + 2 * 4 * kMaxRows;                     // [2][VEC], then nf_w, nf_b
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  const int rl = lane & 31;
+  const int S = p.S;
+  const int MB = (S + 31) >> 5;
+  const int64_t b = blockIdx.x;
+  const float* xb = p.x + b * (int64_t)S * D;
+  float* ob = p.out + b * (int64_t)S * D;
+
+  // ---- residual stream: columns 32w + 8q + 4g + e of row 32mb + rl ----
+  f32x16 xr[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int m = mb * 32 + rl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (m < S) v = *reinterpret_cast<const f32x4*>(xb + (int64_t)m * D + 32 * w + 8 * q + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = v[e];
+    }
+  }
+
+  // ---- weight fragments (A operand): W[n0 + rl][16*kk + 8g .. +8] ----
+  auto wfrag = [&](const f16* W, int K, int n0, int kk) {
+    return *reinterpret_cast<const f16x8*>(W + (int64_t)(n0 + rl) * K + kk * 16 + 8 * g);
+  };
+  // activation fragment (B operand): tile row r, k-step kk (+ chunk offset c0)
+  auto afrag = [&](const char* T, int r, int c0, int kk) {
+    return *reinterpret_cast<const f16x8*>(T + act_off(r, c0 + 2 * kk + g));
+  };
+  auto store_h4 = [&](char* T, int r, int n, const float (&v)[4]) {  // 4 consecutive n at n % 4 == 0
+    const f16x4 t = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *reinterpret_cast<f16x4*>(T + act_off(r, n >> 3) + (n & 7) * 2) = t;
+  };
+
+  // ---- LayerNorm of the residual stream (exact two passes over 4 waves) ----
+  // FINAL: fp32 to the output; else fp16 into the h tile.
+  auto layer_norm = [&](const float* gw, const float* gb, float eps, auto final_c) {
+    constexpr bool FINAL = decltype(final_c)::value;
+    float mean[4], rstd[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += xr[mb][r];
+      s = pair_sum(s);
+      if (g == 0) stats[w * kMaxRows + mb * 32 + rl] = s;
+    }
+    lds_sync();
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = mb * 32 + rl;
+      mean[mb] = (stats[m] + stats[kMaxRows + m] + stats[2 * kMaxRows + m] + stats[3 * kMaxRows + m]) / (float)D;
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float d = xr[mb][r] - mean[mb];
+        s += d * d;
+      }
+      s = pair_sum(s);
+      if (g == 0) stats[4 * kMaxRows + w * kMaxRows + m] = s;
+    }
+    lds_sync();
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = mb * 32 + rl;
+      const float* s2 = stats + 4 * kMaxRows;
+      const float var = (s2[m] + s2[kMaxRows + m] + s2[2 * kMaxRows + m] + s2[3 * kMaxRows + m]) / (float)D;
+      rstd[mb] = 1.0f / sqrtf(var + eps);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = 32 * w + 8 * q + 4 * g;
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(gw + n);
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(gb + n);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int m = mb * 32 + rl;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (xr[mb][4 * q + e] - mean[mb]) * rstd[mb] * wv[e] + bv[e];
+        if constexpr (FINAL) {
+          if (m < S) *reinterpret_cast<f32x4*>(ob + (int64_t)m * D + n) = f32x4{y[0], y[1], y[2], y[3]};
+        } else {
+          store_h4(Ht, m, n, y);
+        }
+      }
+    }
+  };
+
+  f16x8 wq[NQ][KD], wo[KP], w1[KD], w2[KF];
+  auto load_wq = [&](int l) {
+    const f16* W = p.w_qkv + (int64_t)l * 3 * DP * D;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) wq[j][kk] = wfrag(W, D, 32 * (w + 4 * j), kk);
+  };
+  auto load_wo = [&](int l) {
+#pragma unroll
+    for (int kk = 0; kk < KP; ++kk) wo[kk] = wfrag(p.w_o + (int64_t)l * D * DP, DP, 32 * w, kk);
+  };
+  auto load_w1 = [&](int l) {
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) w1[kk] = wfrag(p.w_1 + (int64_t)l * F * D, D, 32 * w, kk);
+  };
+  auto load_w2 = [&](int l) {
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk) w2[kk] = wfrag(p.w_2 + (int64_t)l * D * F, F, 32 * w, kk);
+  };
+
+  // V^T fragment offsets (see flash_dma_body): lane = 16*tq + ts covers
+  // keys 16t + 8r + 4*(tq >> 1) + (ts >> 2), columns 32db + 16*(tq & 1) + 4*(ts & 3).
+  const int tq = lane >> 4, ts = lane & 15;
+  const bool d_ok = HDP % 32 == 0 || rl < HDP;
+  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
+
+  // layer l's vectors: thread t holds elements t + 256*i
+  auto vec_src = [&](int l, int idx) -> float {
+    if (idx < V_BO) return p.b_qkv[(int64_t)l * 3 * DP + idx];
+    if (idx < V_B1) return p.b_o[(int64_t)l * D + idx - V_BO];
+    if (idx < V_B2) return p.b_1[(int64_t)l * F + idx - V_B1];
+    if (idx < V_N1W) return p.b_2[(int64_t)l * D + idx - V_B2];
+    if (idx < V_N1B) return p.n1_w[(int64_t)l * D + idx - V_N1W];
+    if (idx < V_N2W) return p.n1_b[(int64_t)l * D + idx - V_N1B];
+    if (idx < V_N2B) return p.n2_w[(int64_t)l * D + idx - V_N2W];
+    return p.n2_b[(int64_t)l * D + idx - V_N2B];
+  };
+  float vreg[VPT];
+  auto vec_load = [&](int l) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vreg[i] = vec_src(l, threadIdx.x + 256 * i);
+  };
+  auto vec_store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vecs[buf * VEC + threadIdx.x + 256 * i] = vreg[i];
+  };
+  vec_load(0);
+  vec_store(0);
+  if (threadIdx.x < D) {
+    vecs[2 * VEC + threadIdx.x] = p.nf_w[threadIdx.x];
+    vecs[2 * VEC + D + threadIdx.x] = p.nf_b[threadIdx.x];
+  }
+  load_wq(0);
+  lds_sync();  // vectors of layer 0 and the final norm staged
+  layer_norm(vecs + V_N1W, vecs + V_N1B, p.n1_eps, std::false_type{});
+  for (int l = 0; l < p.L; ++l) {
+    lds_sync();  // h complete
+    // ---- QKV = h . W_qkv^T + b -> Q, K, V tiles ----
+    {
+      const float* bq = vecs + (l & 1) * VEC;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= MB) break;
+        f16x8 hf[KD];
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) hf[kk] = afrag(Ht, mb * 32 + rl, 0, kk);
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+          f32x16 acc = {};
+#pragma unroll
+          for (int kk = 0; kk < KD; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[j][kk], hf[kk], acc, 0, 0, 0);
+          const int nb = w + 4 * j;  // 32-column block of [Q | K | V]
+          const int part = nb / (DP / 32), col0 = (nb % (DP / 32)) * 32;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = 32 * nb + 8 * q + 4 * g;
+            const f32x4 bv = *reinterpret_cast<const f32x4*>(bq + n);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[4 * q + e] + bv[e];
+            const int c = col0 + 8 * q + 4 * g, r = mb * 32 + rl;
+            if (part == 2) {
+              const f16x4 t = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+              *reinterpret_cast<f16x4*>(Vt + v_off(r, c >> 3) + (c & 7) * 2) = t;
+            } else {
+              store_h4(part == 0 ? Qt : Kt, r, c, v);
+            }
+          }
+        }
+      }
+    }
+    load_wo(l);
+    if (l + 1 < p.L) vec_load(l + 1);
+    lds_sync();  // Q, K, V complete
+    // ---- attention: heads w, w+4, ...; ctx -> h tile ----
+    for (int hh = w; hh < p.H; hh += 4) {
+      const int hc = hh * HDP / 8;  // first chunk of this head's columns
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        if (qb >= MB) break;
+        const int row = qb * 32 + rl;
+        f16x8 qf[HK];
+#pragma unroll
+        for (int kk = 0; kk < HK; ++kk) qf[kk] = afrag(Qt, row, hc, kk);
+        const int kb_end = CAUSAL ? qb + 1 : MB;
+        f32x16 sacc[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          if (kb < kb_end) {
+            f32x16 a = {};
+#pragma unroll
+            for (int kk = 0; kk < HK; ++kk)
+              a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk), qf[kk], a, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+              if (key >= S || (CAUSAL && key > row)) a[r] = -INFINITY;
+              mx = fmaxf(mx, a[r]);
+            }
+            sacc[kb] = a;
+          }
+        }
+        mx = pair_max(mx);
+        const float cs = p.scale_log2;
+        const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
+        const float m_use = m_tile == -INFINITY ? 0.f : m_tile;
+        f16x8 pf[8];
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          if (kb < kb_end) {
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+              const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(sacc[kb][e], cs, -m_use)),
+                                (f16)__builtin_amdgcn_exp2f(fmaf(sacc[kb][e + 1], cs, -m_use))};
+              pf[2 * kb + (e >> 3)][e & 7] = hp[0];
+              pf[2 * kb + (e >> 3)][(e & 7) + 1] = hp[1];
+              ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+            }
+          }
+        }
+        const float inv = 1.0f / pair_sum(ls);
+        f32x16 oacc[DB];
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          if (t < 2 * kb_end) {
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+              f16x4 half[2];
+#pragma unroll
+              for (int r = 0; r < 2; ++r) {
+                const int vr = 16 * t + 8 * r + 4 * (tq >> 1) + (ts >> 2);
+                const int col = hh * HDP + 32 * d + (HDP >= 32 ? 16 * (tq & 1) : 0) + 4 * (ts & 3);
+                const tr_f16x4 x4 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (lds_tr_f16x4*)(lds_char*)(Vt + v_off(vr, col >> 3) + (col & 7) * 2));
+                half[r] = __builtin_bit_cast(f16x4, x4);
+              }
+              f16x8 vf = __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7);
+              if (!d_ok) vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+              oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], oacc[d], 0, 0, 0);
+            }
+          }
+        }
+        // lane holds O[row][32d + 8q + 4g + e]
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int dd = 32 * d + 8 * q + 4 * g;
+            if (dd < HDP) {
+              const float v[4] = {oacc[d][4 * q] * inv, oacc[d][4 * q + 1] * inv, oacc[d][4 * q + 2] * inv,
+                                  oacc[d][4 * q + 3] * inv};
+              store_h4(Ht, row, hh * HDP + dd, v);
+            }
+          }
+      }
+    }
+    load_w1(l);
+    lds_sync();  // ctx complete
+    // ---- x += ctx . W_o^T + b_o ----
+    {
+      const f32x4* bo4 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_BO + 32 * w + 4 * g);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= MB) break;
+        f32x16 acc = {};
+#pragma unroll
+        for (int kk = 0; kk < KP; ++kk)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wo[kk], afrag(Ht, mb * 32 + rl, 0, kk), acc, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 bv = bo4[2 * q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = xr[mb][4 * q + e] + (acc[4 * q + e] + bv[e]);
+        }
+      }
+    }
+    load_w2(l);
+    layer_norm(vecs + (l & 1) * VEC + V_N2W, vecs + (l & 1) * VEC + V_N2B, p.n2_eps, std::false_type{});
+    lds_sync();  // h complete
+    // ---- u = gelu(h . W_1^T + b_1) -> u tile (reuses Q) ----
+    {
+      const f32x4* b14 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B1 + 32 * w + 4 * g);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= MB) break;
+        f32x16 acc = {};
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1[kk], afrag(Ht, mb * 32 + rl, 0, kk), acc, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 bv = b14[2 * q];
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = gelu_erf(acc[4 * q + e] + bv[e]);
+          store_h4(Qt, mb * 32 + rl, 32 * w + 8 * q + 4 * g, v);
+        }
+      }
+    }
+    if (l + 1 < p.L) {
+      load_wq(l + 1);
+      vec_store((l + 1) & 1);  // layer l+1's vectors (its LN1 runs below)
+    }
+    lds_sync();  // u complete
+    // ---- x += u . W_2^T + b_2 ----
+    {
+      const f32x4* b24 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B2 + 32 * w + 4 * g);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= MB) break;
+        f32x16 acc = {};
+#pragma unroll
+        for (int kk = 0; kk < KF; ++kk)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(w2[kk], afrag(Qt, mb * 32 + rl, 0, kk), acc, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 bv = b24[2 * q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = xr[mb][4 * q + e] + (acc[4 * q + e] + bv[e]);
+        }
+      }
+    }
+    if (l + 1 < p.L)
+      layer_norm(vecs + ((l + 1) & 1) * VEC + V_N1W, vecs + ((l + 1) & 1) * VEC + V_N1B, p.n1_eps,
+                 std::false_type{});
+    else
+      layer_norm(vecs + 2 * VEC, vecs + 2 * VEC + D, p.nf_eps, std::true_type{});
+  }
+}
+
+template <int HDP, bool CAUSAL>
+int launch_small(const SmallArgs& p, int64_t batch, hipStream_t st) {
+  hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, CAUSAL>), dim3((unsigned)batch), dim3(256), 0, st, p);
+  return check_launch("tk_small_forward");
+}
+
+}  // namespace
+}  // namespace tk
+
+using namespace tk;
+
+extern "C" int tk_small_forward_supported(int64_t seq, int64_t d_model, int64_t heads, int64_t head_dim_padded,
+                                          int64_t ffn_dim) {
+  const int64_t hp = head_dim_padded;
+  return seq >= 1 && seq <= kMaxRows && d_model == 128 && ffn_dim == 128 && heads >= 1 &&
+         (hp == 16 || hp == 32 || hp == 64 || hp == 128) && heads * hp == 128;
+}
+
+extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64_t seq, int64_t d_model,
+                                int64_t heads, int64_t head_dim_padded, int64_t ffn_dim, int64_t layers, int causal,
+                                const tk_half* w_qkv, const float* b_qkv, const tk_half* w_o, const float* b_o,
+                                const tk_half* w_1, const float* b_1, const tk_half* w_2, const float* b_2,
+                                const float* n1_w, const float* n1_b, const float* n2_w, const float* n2_b,
+                                const float* nf_w, const float* nf_b, float n1_eps, float n2_eps, float nf_eps,
+                                float scale, void* stream) {
+  clear_error();
+  TK_REQUIRE(x && out && w_qkv && b_qkv && w_o && b_o && w_1 && b_1 && w_2 && b_2 && n1_w && n1_b && n2_w &&
+                 n2_b && nf_w && nf_b,
+             TK_ERR_ARG, "tk_small_forward: null pointer");
+  TK_REQUIRE(tk_small_forward_supported(seq, d_model, heads, head_dim_padded, ffn_dim), TK_ERR_UNSUPPORTED,
+             "tk_small_forward: shape S=%lld D=%lld H=%lld hd=%lld F=%lld outside the kernel's "
+             "(S <= 128, D = F = 128, H*hd = 128, hd in {16,32,64,128})",
+             (long long)seq, (long long)d_model, (long long)heads, (long long)head_dim_padded, (long long)ffn_dim);
+  TK_REQUIRE(batch >= 0 && batch < (1ll << 31) && layers >= 1 && layers < (1 << 20), TK_ERR_ARG,
+             "tk_small_forward: batch=%lld layers=%lld", (long long)batch, (long long)layers);
+  TK_REQUIRE(scale > 0.f, TK_ERR_ARG, "tk_small_forward: scale must be > 0");
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+  TK_REQUIRE(al16(x) && al16(out) && al16(w_qkv) && al16(w_o) && al16(w_1) && al16(w_2) && al16(b_qkv) &&
+                 al16(b_o) && al16(b_1) && al16(b_2) && al16(n1_w) && al16(n1_b) && al16(n2_w) && al16(n2_b) &&
+                 al16(nf_w) && al16(nf_b),
+             TK_ERR_ARG, "tk_small_forward: every buffer must be 16-byte aligned");
+  if (batch == 0) return TK_OK;
+  SmallArgs p;
+  p.x = x;
+  p.out = out;
+  p.w_qkv = reinterpret_cast<const f16*>(w_qkv);
+  p.b_qkv = b_qkv;
+  p.w_o = reinterpret_cast<const f16*>(w_o);
+  p.b_o = b_o;
+  p.w_1 = reinterpret_cast<const f16*>(w_1);
+  p.b_1 = b_1;
+  p.w_2 = reinterpret_cast<const f16*>(w_2);
+  p.b_2 = b_2;
+  p.n1_w = n1_w;
+  p.n1_b = n1_b;
+  p.n2_w = n2_w;
+  p.n2_b = n2_b;
+  p.nf_w = nf_w;
+  p.nf_b = nf_b;
+  p.n1_eps = n1_eps;
+  p.n2_eps = n2_eps;
+  p.nf_eps = nf_eps;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.S = (int)seq;
+  p.L = (int)layers;
+  p.H = (int)heads;
+  hipStream_t st = as_stream(stream);
+  const bool c = causal != 0;
+  switch (head_dim_padded) {
+    case 16: return c ? launch_small<16, true>(p, batch, st) : launch_small<16, false>(p, batch, st);
+    case 32: return c ? launch_small<32, true>(p, batch, st) : launch_small<32, false>(p, batch, st);
+    case 64: return c ? launch_small<64, true>(p, batch, st) : launch_small<64, false>(p, batch, st);
+    default: return c ? launch_small<128, true>(p, batch, st) : launch_small<128, false>(p, batch, st);
+  }
+}

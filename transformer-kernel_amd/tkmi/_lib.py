@@ -54,6 +54,12 @@ SIGNATURES = {
     "tk_masked_softmax": (
         c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]
     ),
+    "tk_small_forward": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int]
+        + [c_void_p] * 14 + [c_float, c_float, c_float, c_float, c_void_p],
+    ),
+    "tk_small_forward_supported": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int64]),
 }
 
 _lock = threading.Lock()

@@ -58,11 +58,15 @@ class OptimizerSettings:
                          forward, so the fused one is kept for narrow rows.
     assume_dense_mask -- skip the one device->host sync per new mask object
                          that checks the padding mask is all-True.
+    small_forward     -- run dense forwards of narrow models (d_model =
+                         ffn_dim = 128, S <= 128) as one whole-forward kernel
+                         (tk_small_forward) instead of the layer loop.
     """
 
     fused_norm: bool = True
     fused_norm_max_d: int = 256
     assume_dense_mask: bool = False
+    small_forward: bool = True
 
 
 _ACTIVE = OptimizerSettings()
@@ -131,6 +135,8 @@ class OptimizedTransformer(BaselineTransformer):
         self.head_dim_padded = _padded_head_dim(self.head_dim)
         self._weight_cache: Optional[List[_LayerWeights]] = None
         self._weight_cache_key: Optional[tuple] = None
+        self._stacked: Optional[dict] = None
+        self._small_ok: dict = {}  # seq -> tk_small_forward_supported
         self._dense_mask_ref: Optional[weakref.ReferenceType] = None
         self._dense_mask_value = False
 
@@ -186,7 +192,27 @@ class OptimizedTransformer(BaselineTransformer):
         self._final = (f32(self.final_norm.weight), f32(self.final_norm.bias), self.final_norm.eps)
         self._weight_cache = built
         self._weight_cache_key = key
+        self._stacked = None
         return built
+
+    def _stacked_weights(self) -> dict:
+        """The per-layer packed weights stacked over layers (tk_small_forward's layout)."""
+        built = self._weights()
+        if self._stacked is None:
+            names = ("w_qkv", "b_qkv", "w_o", "b_o", "w_1", "b_1", "w_2", "b_2", "n1_w", "n1_b", "n2_w", "n2_b")
+            self._stacked = {n: torch.stack([getattr(lw, n) for lw in built]).contiguous() for n in names}
+        return self._stacked
+
+    def _small_forward_ok(self, seq: int, built: List[_LayerWeights]) -> bool:
+        if not self.settings.small_forward or self.head_dim_padded is None:
+            return False
+        if len({lw.n1_eps for lw in built}) != 1 or len({lw.n2_eps for lw in built}) != 1:
+            return False
+        ok = self._small_ok.get(seq)
+        if ok is None:
+            ok = self._small_ok[seq] = ops.small_forward_supported(
+                seq, self.d_model, self.num_heads, self.head_dim_padded, self.config.ffn_dim)
+        return ok
 
     def _mask_is_dense(self, valid_token_mask: Optional[torch.Tensor]) -> bool:
         """True when no token is padded (src/optimized.py:362-389).
@@ -239,6 +265,12 @@ class OptimizedTransformer(BaselineTransformer):
         if xin.dtype != torch.float32:
             xin = xin.float()
         xin = xin.contiguous()
+        if mask is None and self._small_forward_ok(seq, weights):
+            out = torch.empty((bsz, seq, d), dtype=torch.float32, device=dev)
+            ops.small_forward(xin.view(bsz, seq, d), out, self._stacked_weights(), (fn_w, fn_b, fn_eps),
+                              weights[0].n1_eps, weights[0].n2_eps, nh, hd, self.config.ffn_dim,
+                              self.config.causal, self.attn_scale)
+            return out
 
         resid = torch.empty((t, d), dtype=torch.float32, device=dev)
         h = torch.empty((t, d), dtype=torch.float16, device=dev)

@@ -284,6 +284,34 @@ def flash_attention(q, k, v, scale: float, causal: bool, out=None, key_valid=Non
     return out
 
 
+def small_forward_supported(seq: int, d_model: int, heads: int, head_dim_padded: int, ffn_dim: int) -> bool:
+    return bool(_lib.load().tk_small_forward_supported(seq, d_model, heads, head_dim_padded, ffn_dim))
+
+
+def small_forward(x, out, stacked: dict, final: tuple, n1_eps: float, n2_eps: float, heads: int,
+                  head_dim_padded: int, ffn_dim: int, causal: bool, scale: float, name: str = "small_forward"):
+    """The whole dense forward of a narrow model in one launch (tk_small_forward).
+
+    x, out: [B, S, D] fp32 contiguous; ``stacked``: the layers' packed weights
+    stacked over layers (OptimizedTransformer._stacked_weights); ``final`` =
+    (weight, bias, eps) of the final LayerNorm.
+    """
+    _require_cuda(x, out)
+    if x.dtype != torch.float32 or out.dtype != torch.float32 or not x.is_contiguous() or not out.is_contiguous():
+        raise ValueError("small_forward: x and out must be contiguous fp32")
+    b, s, d = x.shape
+    w = stacked
+    layers = w["w_qkv"].shape[0]
+    nf_w, nf_b, nf_eps = final
+    _launch(name, "tk_small_forward", x.data_ptr(), out.data_ptr(), b, s, d, heads, head_dim_padded, ffn_dim,
+            layers, int(causal), w["w_qkv"].data_ptr(), w["b_qkv"].data_ptr(), w["w_o"].data_ptr(),
+            w["b_o"].data_ptr(), w["w_1"].data_ptr(), w["b_1"].data_ptr(), w["w_2"].data_ptr(),
+            w["b_2"].data_ptr(), w["n1_w"].data_ptr(), w["n1_b"].data_ptr(), w["n2_w"].data_ptr(),
+            w["n2_b"].data_ptr(), nf_w.data_ptr(), nf_b.data_ptr(), float(n1_eps), float(n2_eps),
+            float(nf_eps), float(scale), _stream(x))
+    return out
+
+
 def masked_softmax(scores, causal: bool, key_len=None, heads_per_batch: int = 1):
     """fp16 softmax of fp32 ``scores [..., S, S]`` with causal / per-batch key-length masking."""
     _require_cuda(scores)
