@@ -490,7 +490,7 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = p.B * p.H;
   const int n_qt = (p.S + BM - 1) / BM;
   // Heaviest (last) query tiles first; bh fastest so that a head's tiles
@@ -509,7 +509,6 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   const int my_row = q0 + wave * 32 + (lane & 31);
   const int g = lane >> 5;
   const int wave_row_min = q0 + wave * 32;
-  const int wave_row_max = wave_row_min + 31;
 
   // Q^T fragments (B operand): lane supplies Q[row][16*kk + 8*g .. +8].
   f16x8 qf[KSTEPS];
@@ -590,8 +589,6 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
     }
   };
 
-  auto needs = [&](int kt) { return !CAUSAL || kt * kBN <= wave_row_max; };
-
   // ---- S^T = K . Q^T for one tile: two 32-key blocks ----
   auto scores = [&](int stage, f32x16 (&sacc)[2]) {
     const char* ks_ = smem + stage * STAGE;
@@ -612,7 +609,8 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   // accumulator entry r of block kb2 is key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4
   // kbyte: this lane's byte of the tile's key-validity mask (key k0 + lane),
   // loaded one step ahead; the wave ballot turns it into one 64-bit word.
-  auto softmax_pv = [&](int kt, int stage, f32x16 (&sacc)[2], int kbyte) {
+  auto softmax_pv = [&](int kt, int stage, f32x16 (&sacc)[2], int kbyte, bool has_next, int st_next,
+                        f32x16 (&snext)[2]) {
     const int k0 = kt * kBN;
     const char* vs_ = smem + stage * STAGE + KSTAGE;
     const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
@@ -656,16 +654,39 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls = 0.f;
     f16x8 pf[4];
+    // S^T of tile kt+1 (2 x KSTEPS MFMAs, the two key blocks alternating) in
+    // the same region as this tile's 32 exponentials, K operands read RA
+    // ahead; the compiler's scheduler orders the two.  (Pinning a fixed
+    // MFMA/exp interleave with sched_group_barrier measured 1-3 % slower.)
+    constexpr int NSM = 2 * KSTEPS;
+    constexpr int RA = 3;
+    const char* ks_n = smem + st_next * STAGE;
+    f16x8 kfr[NSM];
+    auto rd = [&](int i) {
+      if (has_next)
+        kfr[i] = *reinterpret_cast<const f16x8*>(ks_n + swz_off<KRB>((i & 1) * 32 + (lane & 31), 2 * (i >> 1) + g));
+    };
+    auto sm = [&](int i) {
+      if (has_next) {
+        const int kb2 = i & 1, kk = i >> 1;
+        snext[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr[i], qf[kk], kk == 0 ? f32x16{} : snext[kb2], 0, 0, 0);
+      }
+    };
+    auto ex = [&](int e) {  // entry e: block e / 16, accumulator index e % 16
+      const int kb2 = e >> 4, r = e & 15;
+      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], c, -m_use));
+      ls += pv;
+      pf[kb2 * 2 + (r >> 3)][r & 7] = (f16)pv;
+    };
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+    for (int i = 0; i < RA; ++i) rd(i);
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+    for (int i = 0; i < NSM; ++i) {
+      if (i + RA < NSM) rd(i + RA);
+      sm(i);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][hh * 8 + e], c, -m_use));
-          ls += pv;
-          pf[kb2 * 2 + hh][e] = (f16)pv;
-        }
+      for (int e = (32 * i) / NSM; e < (32 * (i + 1)) / NSM; ++e) ex(e);
+    }
     l_run += ls;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -696,33 +717,47 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   __syncthreads();
 
   f32x16 s_a[2], s_b[2];
-  if (needs(0)) scores(0, s_a);
+  scores(0, s_a);
 
   // One step: prefetch tile kt+2, scores of kt+1 (into s_next), softmax+PV of kt.
   auto key_byte = [&](int kt) { return KMASK ? (int)kvb[min(kt * kBN + lane, p.S - 1)] : 1; };
   int kbyte_cur = key_byte(0);
-  auto step = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_next)[2]) {
+  // Every step runs the softmax and P.V of its tile and the S^T of the next
+  // one unconditionally (a causal tile past a wave's rows is all -inf and
+  // contributes P = 0): MFMAs on conditional paths would make the register
+  // allocator copy their accumulators.  HAS_NEXT is compile-time; the last
+  // step is peeled.
+  auto step = [&](int kt, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], auto next_c) {
+    constexpr bool HAS_NEXT = decltype(next_c)::value;
     const int st_cur = kt % kStages;
     const int st_nxt = (kt + 1) % kStages;
     const int st_pre = (kt + 2) % kStages;
     const bool pre = kt + 2 < n_kt;
     const int kbyte = kbyte_cur;
-    if (kt + 1 < n_kt) kbyte_cur = key_byte(kt + 1);
+    if (HAS_NEXT) kbyte_cur = key_byte(kt + 1);
     if (pre) {
       load_k(kt + 2, st_pre);
       load_v(kt + 2);
     }
-    if (kt + 1 < n_kt && needs(kt + 1)) scores(st_nxt, s_next);
-    if (needs(kt)) softmax_pv(kt, st_cur, s_cur, kbyte);
+    softmax_pv(kt, st_cur, s_cur, kbyte, HAS_NEXT, st_nxt, s_next);
     if (pre) {
       __builtin_amdgcn_s_waitcnt(0);
       store_v(st_pre);
     }
     __syncthreads();
   };
-  for (int kt = 0; kt < n_kt; kt += 2) {
-    step(kt, s_a, s_b);
-    if (kt + 1 < n_kt) step(kt + 1, s_b, s_a);
+  const BoolC<true> T{};
+  const BoolC<false> F{};
+  int kt = 0;
+  for (; kt + 2 < n_kt; kt += 2) {
+    step(kt, s_a, s_b, T);
+    step(kt + 1, s_b, s_a, T);
+  }
+  if (kt + 1 < n_kt) {
+    step(kt, s_a, s_b, T);
+    step(kt + 1, s_b, s_a, F);
+  } else {
+    step(kt, s_a, s_b, F);
   }
 
   // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
