@@ -237,43 +237,32 @@ struct Mainloop {
     lds_barrier();
     read(0, 0, 0);
     int cur = 0;
-    // The MFMA groups run at raised wave priority, so the SIMD's other wave
-    // gets the issue slots only between them (measured: 2-5 % faster at
-    // 256x256 tiles, neutral at 128x128).
     auto ksteps = [&]() {  // k-steps 0 .. KSTEPS-2 of the current K-tile
 #pragma unroll
       for (int kk = 0; kk < KSTEPS - 1; ++kk) {
         read((kk + 1) & 1, cur, kk + 1);
-        __builtin_amdgcn_s_setprio(1);
         mma(kk & 1);
         interleave();
-        __builtin_amdgcn_s_setprio(0);
       }
     };
     // The last K-tile is peeled off: inside the loop the fresh reads of tile
     // kt+1 and the MFMAs of tile kt's last k-step share one block, so the
     // compiler's wait before those MFMAs covers only their own (already
     // complete) fragments instead of also the fresh reads.
-    // After the barrier the last k-step's MFMAs (fragments already in
-    // registers) are issued first and the freed buffer's copies after them,
-    // so the matrix cores restart without waiting behind the copy issue.
     for (int kt = 0; kt < nk - 1; ++kt) {
       ksteps();
       wait_lgkm0();  // this K-tile's fragments are all in registers
       if (kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * INSTS>();
       else wait_vmcnt<0>();
       lds_barrier();
-      const int freed = cur;
-      cur = cur + 1 == STAGES ? 0 : cur + 1;
-      read(0, cur, 0);
-      __builtin_amdgcn_s_setprio(1);
-      mma(1);
-      interleave();  // the fresh reads go out between the MFMAs, not after them
-      __builtin_amdgcn_s_setprio(0);
       if (kt + STAGES < nk) {
 #pragma unroll
-        for (int c = 0; c < INSTS; ++c) copy(kt + STAGES, freed, c);
+        for (int c = 0; c < INSTS; ++c) copy(kt + STAGES, cur, c);
       }
+      cur = cur + 1 == STAGES ? 0 : cur + 1;
+      read(0, cur, 0);
+      mma(1);
+      interleave();  // the fresh reads go out between the MFMAs, not after them
     }
     if (nk > 0) {  // K = 0: no tile, the product is 0
       ksteps();
