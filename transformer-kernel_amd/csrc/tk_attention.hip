@@ -255,7 +255,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
                                             3, 4, 5, 6, 7);
     return d_ok ? f : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   };
-  // O^T += V^T . P^T for a whole tile (the last tile; every tile at head_dim 256).
+  // O^T += V^T . P^T for a whole tile (rescale path and the last tile).
   auto pv_all = [&](const f16x8 (&pf)[4], const char* vs_) {
 #pragma unroll
     for (int c = 0; c < NP; ++c)
@@ -305,17 +305,22 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     // wave has grown by more than 2^8 over it, so exponentials stay <= 256
     // (exact in fp16's range) and the O/l rescale is skipped on most tiles;
     // O and l always share one reference, so the final O/l is unchanged.
-    // l (tiles < kt) is rescaled here; O is rescaled at the end of the step,
-    // after the deferred MFMAs have added tile kt-1 at the old reference, so
-    // no MFMA writes O on a conditional path (an MFMA accumulator written on
-    // two paths is copied between register sets on every step).
-    const bool rescale = __any(m_tile > m_run + 8.0f);
-    float alpha = 1.0f;
-    if (rescale) {
+    // The pending P of tile kt-1 is relative to the old reference: it is
+    // accumulated first and its deferred MFMAs below then add zeros.
+    if (__any(m_tile > m_run + 8.0f)) {
+      if (DEFER && HAS_PREV) {
+        pv_all(p_prev, vslot((kt + kVSlots - 1) % kVSlots));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) p_prev[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
       const float m_new = fmaxf(m_run, m_tile);
-      alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
@@ -389,12 +394,6 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     }
     mx_next = mxn;
     l_run += ls;
-    if (rescale) {
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
-    }
     if (!DEFER) pv_all(p_cur, vslot(kt % kVSlots));
     // keep the copy wait after every MFMA and read of the step
     __builtin_amdgcn_sched_barrier(0);
@@ -430,14 +429,10 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     if (DEFER) pv_all(pf_a, vslot(0));
   } else {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, F);
-    // Two steps per iteration with no branch between them: the loop-carried
-    // accumulators then keep one register assignment.
-    int kt = 1;
-    for (; kt + 1 < n_kt - 1; kt += 2) {
+    for (int kt = 1; kt < n_kt - 1; kt += 2) {
       step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
-      step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
+      if (kt + 1 < n_kt - 1) step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
     }
-    if (kt < n_kt - 1) step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
     const int kl = n_kt - 1;
     if (kl & 1) {
       step(kl, s_b, s_a, pf_b, pf_a, mx_b, mx_a, F, T);
