@@ -186,7 +186,7 @@ def test_flash_rejects_short_key_mask_stride_without_gpu():
 # Attention instantiations the five benchmark configs dispatch:
 # (kernel, head_dim, waves per workgroup, causal) -- C1, C2 (one key tile),
 # C3/C5, C4.
-BENCH_ATTENTION = [("flash_fwd_kernel", 32, 4, 1), ("flash_single_kernel", 64, 2, 0), ("flash_fwd_kernel", 64, 8, 1),
+BENCH_ATTENTION = [("flash_fwd_kernel", 32, 4, 1), ("flash_single_kernel", 64, 2, 0), ("flash_fwd_kernel", 64, 4, 1),
                    ("flash_fwd_kernel", 128, 8, 1)]
 
 

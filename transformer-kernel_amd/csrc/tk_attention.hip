@@ -255,7 +255,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
                                             3, 4, 5, 6, 7);
     return d_ok ? f : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   };
-  // O^T += V^T . P^T for a whole tile (rescale path and the last tile).
+  // O^T += V^T . P^T for a whole tile (the last tile; every tile at head_dim 256).
   auto pv_all = [&](const f16x8 (&pf)[4], const char* vs_) {
 #pragma unroll
     for (int c = 0; c < NP; ++c)
@@ -305,22 +305,24 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     // wave has grown by more than 2^8 over it, so exponentials stay <= 256
     // (exact in fp16's range) and the O/l rescale is skipped on most tiles;
     // O and l always share one reference, so the final O/l is unchanged.
-    // The pending P of tile kt-1 is relative to the old reference: it is
-    // accumulated first and its deferred MFMAs below then add zeros.
-    if (__any(m_tile > m_run + 8.0f)) {
-      if (DEFER && HAS_PREV) {
-        pv_all(p_prev, vslot((kt + kVSlots - 1) % kVSlots));
-#pragma unroll
-        for (int t = 0; t < 4; ++t) p_prev[t] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
+    // l (tiles < kt) is rescaled here.  With deferred P.V, O is rescaled at
+    // the end of the step, after the deferred MFMAs have added tile kt-1 at
+    // the old reference, so no MFMA writes O on a conditional path (an MFMA
+    // accumulator written on two paths is copied between register sets on
+    // every step); without deferral (head_dim 256) it is rescaled here.
+    const bool rescale = __any(m_tile > m_run + 8.0f);
+    float alpha = 1.0f;
+    if (rescale) {
       const float m_new = fmaxf(m_run, m_tile);
-      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
+      if constexpr (!DEFER) {  // no pending P: O is rescaled here (fewer spills at head_dim 256)
 #pragma unroll
-      for (int d = 0; d < DB; ++d)
+        for (int d = 0; d < DB; ++d)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+          for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+      }
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
@@ -394,6 +396,12 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     }
     mx_next = mxn;
     l_run += ls;
+    if (DEFER && rescale) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+    }
     if (!DEFER) pv_all(p_cur, vslot(kt % kVSlots));
     // keep the copy wait after every MFMA and read of the step
     __builtin_amdgcn_sched_barrier(0);
@@ -429,9 +437,20 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     if (DEFER) pv_all(pf_a, vslot(0));
   } else {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, F);
-    for (int kt = 1; kt < n_kt - 1; kt += 2) {
-      step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
-      if (kt + 1 < n_kt - 1) step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
+    if constexpr (DEFER) {
+      // Two steps per iteration with no branch between them: the loop-carried
+      // accumulators then keep one register assignment.
+      int kt = 1;
+      for (; kt + 1 < n_kt - 1; kt += 2) {
+        step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
+        step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
+      }
+      if (kt < n_kt - 1) step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
+    } else {  // head_dim 256: this shape spills less there
+      for (int kt = 1; kt < n_kt - 1; kt += 2) {
+        step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
+        if (kt + 1 < n_kt - 1) step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
+      }
     }
     const int kl = n_kt - 1;
     if (kl & 1) {
@@ -926,12 +945,15 @@ __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
   }
 }
 
-// Short sequences (NW <= 4) at head_dim <= 32 ask for two waves per SIMD:
-// left alone the compiler spends 280-300 registers on them (one wave per
-// SIMD), and these launches are latency-bound (b256 s64 d32: 14.4 -> 12.4
-// us).  At head_dim 64 the same bound spills, so it is not applied there.
+// Four-wave workgroups at head_dim <= 64 ask for two waves per SIMD (two
+// workgroups per CU): left alone the compiler spends 280-370 registers on
+// them (one wave per SIMD).  With two independent workgroups per CU one
+// workgroup's prologue and epilogue overlap the other's steady state, which
+// is why long sequences also run 128-row (four-wave) query tiles at these
+// head dims (measured against 256-row tiles, one workgroup per CU: b8 s2048
+// causal 129 -> 118 us, b2 s32768 causal 5.81 -> 5.73 ms).
 template <int HD, int NW, bool CAUSAL, bool KMASK>
-__global__ __launch_bounds__(NW * 64, (NW <= 4 && HD <= 32) ? 2 : 1) void flash_fwd_kernel(AttnArgs p) {
+__global__ __launch_bounds__(NW * 64, (NW <= 4 && HD <= 64) ? 2 : 1) void flash_fwd_kernel(AttnArgs p) {
   if constexpr (HD == 128) flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
   else flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
 }
@@ -972,15 +994,17 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   return check_launch("tk_flash_attn_fwd");
 }
 
-// Query rows per workgroup: 256 (8 waves sharing each K/V tile) for long
-// sequences, fewer when S is short so no wave idles on padding rows; one key
-// tile (S <= 64) at head_dim <= 64 takes flash_single_body.
+// Query rows per workgroup: at head_dim 128, 256 (8 waves sharing each K/V
+// tile, one workgroup per CU) for long sequences; at head_dim <= 64, 128
+// (4 waves, two workgroups per CU); fewer when S is short so no wave idles
+// on padding rows; one key tile (S <= 64) at head_dim <= 64 takes
+// flash_single_body.
 template <int HD>
 int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   if constexpr (HD == 256) {  // one wave per SIMD: at most four waves (128 rows)
     if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   } else {
-    if (p.S > 128) return launch_flash<HD, 8>(p, causal, st);
+    if (p.S > 128) return launch_flash<HD, HD <= 64 ? 4 : 8>(p, causal, st);
     if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   }
   if constexpr (HD <= 64) return launch_single<HD>(p, causal, st);
