@@ -91,6 +91,9 @@ def kernel_units(name: str, cfg) -> tuple:
         pairs = s * (s + 1) / 2 if causal else s * s
         per_layer = 2.0 * t * (3 * d * d + d * d + 2 * d * f) + 4.0 * b * d * pairs
         return per_layer * cfg[5], "flop", "mfma"
+    if name == "qkv_attn":  # fused QKV projection + one-tile attention
+        pairs = s * (s + 1) / 2 if causal else s * s
+        return 2.0 * t * 3 * d * d + 4.0 * b * d * pairs, "flop", "mfma"
     if name == "flash_attn":
         if s <= 64:  # one key tile per head: Q, K, V read and O written once (fp16)
             return 8.0 * t * d, "byte", "hbm"

@@ -206,6 +206,28 @@ int tk_small_forward(const float *x, float *out, int64_t batch, int64_t seq,
                      const float *nf_w, const float *nf_b, float n1_eps,
                      float n2_eps, float nf_eps, float scale, void *stream);
 
+/* Fused QKV projection + attention for one-key-tile sequences:
+ *   ctx[t, h*64 + :64] = attention_h( h . W_qkv^T + b_qkv )
+ * i.e. tk_gemm(h, w_qkv, b_qkv) into a [T, 3*d_model] q|k|v buffer followed
+ * by tk_flash_attn_fwd on its strided views, without the buffer: q, k and v
+ * of one head for two sequences stay in LDS.  h: [batch*seq, ldh] fp16;
+ * w_qkv: [3*d_model, ldw] fp16 (rows q, k, v, each head's 64 rows
+ * contiguous); b_qkv: [3*d_model] fp32; ctx: [batch*seq, ldc] fp16;
+ * d_model = heads * head_dim.  Dense inputs only.  Shapes:
+ * tk_qkv_attention_supported (seq = 64, head_dim = 64, batch*seq a multiple
+ * of 128).  Replaces F.linear + scaled_dot_product_attention of
+ * OptimizedTransformer._attention_block (src/optimized.py:572-626) for those
+ * shapes (the reference's config 2). */
+int tk_qkv_attention(const tk_half *h, int64_t ldh, const tk_half *w_qkv,
+                     int64_t ldw, const float *b_qkv, tk_half *ctx,
+                     int64_t ldc, int64_t batch, int64_t seq, int64_t heads,
+                     int64_t head_dim, float scale, int causal, void *stream);
+
+/* 1 when tk_qkv_attention takes the shape, else 0.  No counterpart in the
+ * reference (its attention block always materialises q, k, v). */
+int tk_qkv_attention_supported(int64_t batch, int64_t seq, int64_t heads,
+                               int64_t head_dim);
+
 /* 1 when tk_small_forward takes the shape (seq <= 128, d_model = ffn_dim =
  * 128, heads * head_dim_padded = 128, head_dim_padded in {16, 32, 64, 128}),
  * else 0.  No counterpart in the reference (its narrow configs run the

@@ -35,38 +35,13 @@
 // into one FMA before exp2: exp2(s*c - m*c) = exp(scale*(s - m))), -inf
 // masking of future and invalid keys, fp32 running max and sums, fp16 P for
 // the PV product, fp32 accumulation, one final divide.
-#include "tk_common.hpp"
+#include "tk_attn_tile.hpp"
 
 namespace tk {
 namespace {
 
 constexpr int kBN = 64;     // keys per tile
 constexpr int kKSlots = 2;  // flash_dma_body K tiles in LDS: t+1 (read), t+2 (landing)
-
-
-// LDS byte offset of the 16-byte chunk `chunk` of row `row` in a K tile
-// whose rows are RB bytes long.  The gfx950 LDS serves 16-byte-per-lane
-// accesses for 16 lanes per cycle from one 256-byte line of 64 banks, so the
-// chunk index is XOR-ed with the row's line number (modulo the chunks per
-// row): 16 consecutive rows read at one logical chunk then hit 16 distinct
-// 16-byte bank groups.
-template <int RB>
-__device__ __forceinline__ int swz_off(int row, int chunk) {
-  if constexpr (RB >= 256) return row * RB + ((chunk ^ (row & 15)) << 4);
-  else if constexpr (RB == 128) return row * RB + ((chunk ^ ((row >> 1) & 7)) << 4);
-  else if constexpr (RB == 64) return row * RB + ((chunk ^ ((row >> 2) & 3)) << 4);
-  else return row * RB + ((chunk ^ ((row >> 3) & 1)) << 4);
-}
-
-// Chunk XOR of a V tile row for the transposed reads: the four rows a
-// half-wave reads (r0..r0+3, r0 % 4 == 0) must put the 32 bytes each of them
-// contributes on distinct banks.  Rows of 64 or 32 bytes already do.
-template <int RB>
-__device__ __forceinline__ int vswz(int row) {
-  if constexpr (RB >= 256) return 4 * (row & 3);
-  else if constexpr (RB == 128) return 4 * ((row >> 1) & 1);
-  else return 0;
-}
 
 
 // s_waitcnt vmcnt(0) with the other counters unconstrained (gfx9 encoding).
@@ -811,10 +786,7 @@ __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
   constexpr int COPIES = TILE / 1024;      // 1 KB wave copies per tile
   constexpr int CPW = (COPIES + NW - 1) / NW;
   constexpr int RPC = 1024 / RB;           // tile rows per copy
-  constexpr int DB = (HD + 31) / 32;       // 32-row blocks of the O^T accumulator
   constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
-  constexpr int NS = 2 * KSTEPS;           // S^T MFMAs
-  constexpr int NP = 4 * DB;               // O^T MFMAs
   static_assert(HD <= 64 && BM >= kBN, "one key tile, every query row in the workgroup");
   static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
 
@@ -863,86 +835,8 @@ __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
   wait_copies();
   __syncthreads();
 
-  // ---- S^T = K . Q^T: entry r of block kb2 is key 32*kb2 + 8*(r/4) + 4*g + r%4 ----
-  f32x16 s[2];
-#pragma unroll
-  for (int c = 0; c < NS; ++c) {
-    const int kb2 = c / KSTEPS, kk = c % KSTEPS;
-    const f16x8 kf = *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>(kb2 * 32 + (lane & 31), 2 * kk + g));
-    s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], kk == 0 ? f32x16{} : s[kb2], 0, 0, 0);
-  }
-  float mx = -INFINITY;
-  const uint64_t kb64 = kbits >> (4 * g);
-#pragma unroll
-  for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
-      const int key = j + 4 * g;
-      if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kb64 >> j) & 1) == 0)) s[kb2][r] = -INFINITY;
-      mx = fmaxf(mx, s[kb2][r]);
-    }
-  mx = pair_max(mx);
-  const float cs = p.scale_log2;
-  const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
-  const float m_use = m_tile == -INFINITY ? 0.f : m_tile;
-
-  // ---- P in fp16 (8 consecutive entries = one B operand) and its row sum ----
-  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
-  f16x8 pf[4];
-  float ls = 0.f;
-#pragma unroll
-  for (int e = 0; e < 32; e += 2) {
-    const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use)),
-                      (f16)__builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use))};
-    pf[e >> 3][e & 7] = hp[0];
-    pf[e >> 3][(e & 7) + 1] = hp[1];
-    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
-  }
-
-  // ---- O^T = V^T . P^T; V^T operands by transposed LDS reads (see flash_dma_body) ----
-  int v_rd[2][DB];
-  {
-    const int tq = lane >> 4, ts = lane & 15;
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
-        const int col = 32 * d + (HD >= 32 ? 16 * (tq & 1) : 0) + 4 * (ts & 3);  // HD 16: lanes >= 16 are zeroed
-        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
-      }
-  }
-  const bool d_ok = HD % 32 == 0 || (lane & 31) < HD;
-  f32x16 acc_o[DB];
-#pragma unroll
-  for (int c = 0; c < NP; ++c) {
-    const int t = c / DB, d = c % DB;
-    const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
-    const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
-    const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
-    f16x8 vf = __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2, 3, 4,
-                                       5, 6, 7);
-    if (!d_ok) vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    acc_o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], t == 0 ? f32x16{} : acc_o[d], 0, 0, 0);
-  }
-
-  // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
-  const float inv = 1.0f / pair_sum(ls);
-  if (my_row < p.S) {
-    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int dd = d * 32 + 8 * q + 4 * g;
-        if (dd < HD) {
-          f16x4 t = {(f16)(acc_o[d][4 * q] * inv), (f16)(acc_o[d][4 * q + 1] * inv),
-                     (f16)(acc_o[d][4 * q + 2] * inv), (f16)(acc_o[d][4 * q + 3] * inv)};
-          *reinterpret_cast<f16x4*>(ob + dd) = t;
-        }
-      }
-  }
+  attend_one_tile<HD, CAUSAL, KMASK>(ks_, vs_, qf, my_row, p.S, kbits, p.scale_log2,
+                                     p.o + b * p.os[0] + h * p.os[1], p.os[2]);
 }
 
 // Four-wave workgroups at head_dim <= 64 ask for two waves per SIMD (two

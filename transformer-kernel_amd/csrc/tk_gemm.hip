@@ -20,7 +20,7 @@
 // remapped so that the tiles of one XCD (workgroups are dealt round-robin
 // over the 8 XCDs) form a compact group of output tiles sharing A rows and
 // W rows in that XCD's L2.
-#include "tk_common.hpp"
+#include "tk_attn_tile.hpp"
 
 namespace tk {
 namespace {
@@ -44,6 +44,7 @@ struct GemmArgs {
   float eps;
   bool vec;     // output rows admit 4-wide vector stores
   bool bias16;  // bias is 16-byte aligned
+  int64_t w_gstride;  // grouped W rows (Mainloop WG > 0): group stride in rows
 };
 
 // LDS tile layout: rows of BK halves (BK = 64: 128 bytes = eight 16-byte
@@ -117,7 +118,10 @@ __device__ __forceinline__ void wait_lgkm0() {
 // so the matrix cores keep working across the barrier.
 // Staged (K tail): 16-byte register prefetch of the next tile with zero fill
 // past M, N, K, two LDS buffers.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT>
+// WG > 0 (direct path only): the tile's W rows come in groups of WG rows,
+// group k starting at global row n0 + k * p.w_gstride (the q, k and v rows of
+// one head in the fused QKV weight); every row must exist.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT, int WG = 0>
 struct Mainloop {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = 64 * NW;
@@ -138,6 +142,7 @@ struct Mainloop {
   static_assert(KSTEPS % 2 == 0, "even number of k-steps per K-tile");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(DIRECT || STAGES == 2, "the staged path double-buffers");
+  static_assert(WG == 0 || (DIRECT && BN % WG == 0), "grouped W rows: direct path, whole groups");
   static_assert(!DIRECT || (BM % (RPC * NW) == 0 && BN % (RPC * NW) == 0), "copies must divide waves");
   static_assert(DIRECT || ((BM * CPR) % NT == 0 && (BN * CPR) % NT == 0), "chunks must divide threads");
   static_assert((STAGES - 1) * INSTS < 64, "vmcnt range");
@@ -180,7 +185,10 @@ struct Mainloop {
     for (int i = 0; i < W_INSTS; ++i) {
       const int r = (wave * W_INSTS + i) * RPC + lane / CPR;
       const int c = swz<BK>(r, lane % CPR) - r * BK;
-      gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
+      if constexpr (WG > 0)
+        gw[i] = p.w + (n0 + (int64_t)(r / WG) * p.w_gstride + r % WG) * p.ldw + c;
+      else
+        gw[i] = p.w + (int64_t)min(n0 + r, p.N - 1) * p.ldw + c;
     }
     // Wave copy c of tile kt into `stage`: copies 0..A_INSTS-1 are A rows,
     // the rest W rows, 1 KB each.
@@ -796,6 +804,84 @@ int launch_gemm_ln(const GemmArgs& p, bool h_half, hipStream_t st) {
   return check_launch("tk_gemm_bias_add_ln");
 }
 
+// ---- fused QKV projection + one-tile attention (S = 64, head_dim = 64) ----
+// One workgroup computes, for 128 tokens (two sequences) and one head h, the
+// 128 x 192 tile [Q_h | K_h | V_h] = h . [Wq_h | Wk_h | Wv_h]^T + b (fp32
+// accumulate, bias in fp32, fp16 rounding -- the values the plain QKV GEMM
+// would store), stages it in LDS in the single-tile attention layouts and
+// runs that attention for both sequences (waves 2s, 2s+1: query rows 0-31
+// and 32-63 of sequence s).  Q, K and V never reach HBM; only the context
+// [tokens, d_model] is written.  Results are those of the QKV GEMM followed
+// by the single-tile flash kernel.
+constexpr int kQaHD = 64;                 // head_dim
+constexpr int kQaS = 64;                  // sequence length (one key tile)
+constexpr int kQaRows = 128;              // tokens per workgroup
+constexpr int kQaTile = kQaS * kQaHD * 2; // bytes of one K or V tile
+using QaLoop = Mainloop<kQaRows, 3 * kQaHD, 2, 2, 64, 2, true, kQaHD>;
+
+struct QaArgs {
+  f16* ctx;
+  int64_t ldo;
+  int H;
+  float scale_log2;
+};
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void qkv_attn_kernel(GemmArgs p, QaArgs a) {
+  static_assert(QaLoop::FM == 2 && QaLoop::FN == 3 && QaLoop::NW == 4, "4 waves of 64 x 96");
+  __shared__ __attribute__((aligned(16))) f16 smem[QaLoop::LDS_HALVES];
+  static_assert(QaLoop::LDS_HALVES * 2 >= kQaRows * kQaHD * 2 + 4 * kQaTile, "Q, K and V staging fits");
+  const int tiles_m = p.M / kQaRows;
+  int tm, h;
+  tile_of_block(blockIdx.x, tiles_m, a.H, tm, h);
+  const int m0 = tm * kQaRows;
+  f32x16 acc[QaLoop::FN][QaLoop::FM];
+  QaLoop::run(p, m0, h * kQaHD, smem, acc);
+
+  char* lds = reinterpret_cast<char*>(smem);
+  char* q_s = lds;                                 // [128 rows][128 B], chunk-swizzled
+  char* k_s = lds + kQaRows * kQaHD * 2;           // two K tiles
+  char* v_s = k_s + 2 * kQaTile;                   // two V tiles
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave % 2, wn = wave / 2;
+  const int g = lane >> 5;
+  __syncthreads();  // every wave is done with the main-loop buffers
+  // accumulator element (i, j, 4q+e): row wm*64 + 32j + (lane & 31),
+  // column wn*96 + 32i + 8q + 4g + e of [Q | K | V]
+#pragma unroll
+  for (int i = 0; i < QaLoop::FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = wn * 96 + i * 32 + 8 * q + 4 * g;
+      const int part = n / kQaHD, d = n % kQaHD;  // 0 Q, 1 K, 2 V
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(p.bias + (int64_t)part * p.w_gstride + h * kQaHD + d);
+#pragma unroll
+      for (int j = 0; j < QaLoop::FM; ++j) {
+        const int m = wm * 64 + j * 32 + (lane & 31);
+        const f16x4 t = {(f16)(acc[i][j][4 * q] + bv[0]), (f16)(acc[i][j][4 * q + 1] + bv[1]),
+                         (f16)(acc[i][j][4 * q + 2] + bv[2]), (f16)(acc[i][j][4 * q + 3] + bv[3])};
+        const int sq = m / kQaS, r = m % kQaS;
+        char* dst;
+        if (part == 0) dst = q_s + swz_off<2 * kQaHD>(m, d >> 3) + (d & 7) * 2;
+        else if (part == 1) dst = k_s + sq * kQaTile + swz_off<2 * kQaHD>(r, d >> 3) + (d & 7) * 2;
+        else dst = v_s + sq * kQaTile + r * (2 * kQaHD) + (((d >> 3) ^ vswz<2 * kQaHD>(r)) << 4) + (d & 7) * 2;
+        *reinterpret_cast<f16x4*>(dst) = t;
+      }
+    }
+  __syncthreads();
+
+  const int sq = wave / 2;                      // sequence of this wave
+  const int my_row = (wave % 2) * 32 + (lane & 31);
+  f16x8 qf[kQaHD / 16];
+#pragma unroll
+  for (int kk = 0; kk < kQaHD / 16; ++kk)
+    qf[kk] = *reinterpret_cast<const f16x8*>(q_s + swz_off<2 * kQaHD>(sq * kQaS + my_row, 2 * kk + g));
+  attend_one_tile<kQaHD, CAUSAL, false>(k_s + sq * kQaTile, v_s + sq * kQaTile, qf, my_row, kQaS, 0ull,
+                                        a.scale_log2, a.ctx + (int64_t)(m0 + sq * kQaS) * a.ldo + h * kQaHD,
+                                        a.ldo);
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
@@ -891,4 +977,40 @@ extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half*
   if (n == 512) return launch_gemm_ln<Tile<64, 512, 1, 8, 64, 2>>(p, hh, st);
   if (n == 256) return launch_gemm_ln<Tile<64, 256, 1, 4, 64, 2>>(p, hh, st);
   return launch_gemm_ln<Tile<64, 128, 1, 2, 64, 2>>(p, hh, st);
+}
+
+extern "C" int tk_qkv_attention_supported(int64_t batch, int64_t seq, int64_t heads, int64_t head_dim) {
+  return seq == kQaS && head_dim == kQaHD && heads >= 1 && batch >= 0 && (batch * seq) % kQaRows == 0;
+}
+
+extern "C" int tk_qkv_attention(const tk_half* h, int64_t ldh, const tk_half* w_qkv, int64_t ldw,
+                                const float* b_qkv, tk_half* ctx, int64_t ldc, int64_t batch, int64_t seq,
+                                int64_t heads, int64_t head_dim, float scale, int causal, void* stream) {
+  TK_REQUIRE(h && w_qkv && b_qkv && ctx, TK_ERR_ARG, "tk_qkv_attention: null pointer");
+  TK_REQUIRE(tk_qkv_attention_supported(batch, seq, heads, head_dim), TK_ERR_UNSUPPORTED,
+             "tk_qkv_attention: needs seq=%d, head_dim=%d and batch*seq a multiple of %d (got batch=%lld "
+             "seq=%lld head_dim=%lld)",
+             kQaS, kQaHD, kQaRows, (long long)batch, (long long)seq, (long long)head_dim);
+  const int64_t d = heads * head_dim;
+  TK_REQUIRE(d < (1 << 20) && batch * seq < (1ll << 31), TK_ERR_ARG, "tk_qkv_attention: bad sizes");
+  TK_REQUIRE(ldh >= d && ldh % 8 == 0 && ldw >= d && ldw % 8 == 0 && ldc >= d && ldc % 4 == 0, TK_ERR_ARG,
+             "tk_qkv_attention: ldh, ldw must be multiples of 8 and ldc of 4, each >= d_model");
+  TK_REQUIRE(aligned16(h) && aligned16(w_qkv) && aligned16(b_qkv) && ((uintptr_t)ctx & 7) == 0, TK_ERR_ARG,
+             "tk_qkv_attention: h, w_qkv, b_qkv need 16-byte and ctx 8-byte alignment");
+  if (batch == 0) return TK_OK;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const f16*>(h);
+  p.w = reinterpret_cast<const f16*>(w_qkv);
+  p.bias = b_qkv;
+  p.lda = ldh;
+  p.ldw = ldw;
+  p.M = (int)(batch * seq);
+  p.N = (int)(3 * d);
+  p.K = (int)d;
+  p.w_gstride = d;
+  QaArgs qa{reinterpret_cast<f16*>(ctx), ldc, (int)heads, scale * 1.4426950408889634f};
+  const dim3 grid((unsigned)((int64_t)(p.M / kQaRows) * heads)), block(256);
+  if (causal) hipLaunchKernelGGL((qkv_attn_kernel<true>), grid, block, 0, as_stream(stream), p, qa);
+  else hipLaunchKernelGGL((qkv_attn_kernel<false>), grid, block, 0, as_stream(stream), p, qa);
+  return check_launch("tk_qkv_attention");
 }

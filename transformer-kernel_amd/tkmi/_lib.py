@@ -51,6 +51,12 @@ SIGNATURES = {
          c_void_p, c_int64, c_void_p],
     ),
     "tk_attention_supported": (c_int, [c_int64]),
+    "tk_qkv_attention": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
+         c_float, c_int, c_void_p],
+    ),
+    "tk_qkv_attention_supported": (c_int, [c_int64, c_int64, c_int64, c_int64]),
     "tk_masked_softmax": (
         c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]
     ),

@@ -21,7 +21,9 @@ reference schedule it replaces):
   5. FFN-down GEMM  + residual + LayerNorm(next) + cast -> resid fp32, h fp16
                     (the last layer's applies final_norm and writes fp32 out)
 
-plus one LayerNorm before the first layer.  Steps 3 and 5 run as one kernel
+plus one LayerNorm before the first layer.  For one-key-tile sequences (S =
+64, head_dim 64; the reference's config 2) steps 1 and 2 run as one kernel
+that keeps q, k and v on chip.  Steps 3 and 5 run as one kernel
 when a whole row fits a GEMM tile and is narrow enough for that to pay
 (d_model <= OptimizerSettings.fused_norm_max_d); otherwise as a
 residual-epilogue GEMM followed by the standalone LayerNorm kernel.  The
@@ -61,12 +63,16 @@ class OptimizerSettings:
     small_forward     -- run dense forwards of narrow models (d_model =
                          ffn_dim = 128, S <= 128) as one whole-forward kernel
                          (tk_small_forward) instead of the layer loop.
+    qkv_attention     -- for dense one-key-tile sequences (S = 64, head_dim
+                         64) run the QKV projection and attention as one
+                         kernel (tk_qkv_attention), q/k/v kept on chip.
     """
 
     fused_norm: bool = True
     fused_norm_max_d: int = 256
     assume_dense_mask: bool = False
     small_forward: bool = True
+    qkv_attention: bool = True
 
 
 _ACTIVE = OptimizerSettings()
@@ -274,7 +280,9 @@ class OptimizedTransformer(BaselineTransformer):
 
         resid = torch.empty((t, d), dtype=torch.float32, device=dev)
         h = torch.empty((t, d), dtype=torch.float16, device=dev)
-        qkv = torch.empty((t, 3 * dp), dtype=torch.float16, device=dev)
+        fused_qa = (mask is None and self.settings.qkv_attention
+                    and ops.qkv_attention_supported(bsz, seq, nh, hd))
+        qkv = None if fused_qa else torch.empty((t, 3 * dp), dtype=torch.float16, device=dev)
         ctx = torch.empty((t, dp), dtype=torch.float16, device=dev)
         u = torch.empty((t, self.config.ffn_dim), dtype=torch.float16, device=dev)
         out = torch.empty((t, d), dtype=torch.float32, device=dev)
@@ -285,13 +293,18 @@ class OptimizedTransformer(BaselineTransformer):
         ops.ln_fwd(xin, weights[0].n1_w, weights[0].n1_b, weights[0].n1_eps, torch.float16, out=h,
                    name="ln_in")
         src = xin  # residual stream input of the next add (the caller's x is never written)
-        qkv5 = qkv.view(bsz, seq, 3, nh, hd)
-        q, k, v = qkv5.permute(2, 0, 3, 1, 4).unbind(0)  # [B, H, S, hd] strided views
+        if qkv is not None:
+            qkv5 = qkv.view(bsz, seq, 3, nh, hd)
+            q, k, v = qkv5.permute(2, 0, 3, 1, 4).unbind(0)  # [B, H, S, hd] strided views
         ctx3 = ctx.view(bsz, seq, dp)
         last = len(weights) - 1
         for i, lw in enumerate(weights):
-            ops.linear(h, lw.w_qkv, lw.b_qkv, out=qkv, name="qkv")
-            ops.flash_attention(q, k, v, self.attn_scale, self.config.causal, out=ctx3, key_valid=mask)
+            if fused_qa:
+                ops.qkv_attention(h, lw.w_qkv, lw.b_qkv, bsz, seq, nh, hd, self.attn_scale, self.config.causal,
+                                  out=ctx)
+            else:
+                ops.linear(h, lw.w_qkv, lw.b_qkv, out=qkv, name="qkv")
+                ops.flash_attention(q, k, v, self.attn_scale, self.config.causal, out=ctx3, key_valid=mask)
             if fuse:
                 ops.linear_add_ln(ctx, lw.w_o, lw.b_o, src, lw.n2_w, lw.n2_b, lw.n2_eps,
                                   sum_out=resid, h_out=h, name="out_proj_ln",

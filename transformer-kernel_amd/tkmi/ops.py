@@ -284,6 +284,35 @@ def flash_attention(q, k, v, scale: float, causal: bool, out=None, key_valid=Non
     return out
 
 
+def qkv_attention_supported(batch: int, seq: int, heads: int, head_dim: int) -> bool:
+    return bool(_lib.load().tk_qkv_attention_supported(batch, seq, heads, head_dim))
+
+
+def qkv_attention(h, w_qkv, b_qkv, batch: int, seq: int, heads: int, head_dim: int, scale: float,
+                  causal: bool, out=None, name: str = "qkv_attn"):
+    """Fused ``F.linear(h, w_qkv, b_qkv)`` + attention for one-key-tile sequences.
+
+    ``h`` [batch*seq, d] fp16, ``w_qkv`` [3d, d] fp16 (q, k, v rows), ``b_qkv``
+    [3d] fp32; returns the context ``[batch*seq, d]`` fp16 -- what
+    ``linear`` into a q|k|v buffer followed by ``flash_attention`` on its
+    views gives (src/optimized.py:572-626), without the q|k|v buffer.
+    """
+    _require_cuda(h, w_qkv, b_qkv)
+    _check_gemm_operands(h, w_qkv)
+    d = heads * head_dim
+    if tuple(h.shape) != (batch * seq, d) or tuple(w_qkv.shape) != (3 * d, d) or tuple(b_qkv.shape) != (3 * d,):
+        raise ValueError("qkv_attention: h [B*S, d], w_qkv [3d, d], b_qkv [3d] expected")
+    if b_qkv.dtype != torch.float32 or not b_qkv.is_contiguous():
+        raise TypeError("qkv_attention: b_qkv must be contiguous fp32")
+    if out is None:
+        out = torch.empty((batch * seq, d), dtype=torch.float16, device=h.device)
+    _launch(
+        name, "tk_qkv_attention", h.data_ptr(), h.stride(0), w_qkv.data_ptr(), w_qkv.stride(0), b_qkv.data_ptr(),
+        out.data_ptr(), out.stride(0), batch, seq, heads, head_dim, float(scale), int(bool(causal)), _stream(h),
+    )
+    return out
+
+
 def small_forward_supported(seq: int, d_model: int, heads: int, head_dim_padded: int, ffn_dim: int) -> bool:
     return bool(_lib.load().tk_small_forward_supported(seq, d_model, heads, head_dim_padded, ffn_dim))
 
