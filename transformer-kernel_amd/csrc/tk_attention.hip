@@ -890,15 +890,22 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 
 // Query rows per workgroup: at head_dim 128, 256 (8 waves sharing each K/V
 // tile, one workgroup per CU) for long sequences; at head_dim <= 64, 128
-// (4 waves, two workgroups per CU); fewer when S is short so no wave idles
-// on padding rows; one key tile (S <= 64) at head_dim <= 64 takes
-// flash_single_body.
+// (4 waves, two workgroups per CU) up to kLongS keys and 256 beyond -- every
+// query tile streams its key prefix, so halving the tile doubles that
+// traffic, and past ~32k keys the kernel becomes bound by it (b32 s100000:
+// 128-row tiles 16 % slower; b2 s32768: 1 % faster); fewer rows when S is
+// short so no wave idles on padding rows; one key tile (S <= 64) at
+// head_dim <= 64 takes flash_single_body.
+constexpr int kLongS = 32768;
 template <int HD>
 int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
   if constexpr (HD == 256) {  // one wave per SIMD: at most four waves (128 rows)
     if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   } else {
-    if (p.S > 128) return launch_flash<HD, HD <= 64 ? 4 : 8>(p, causal, st);
+    if (p.S > 128) {
+      if (HD <= 64 && p.S <= kLongS) return launch_flash<HD, 4>(p, causal, st);
+      return launch_flash<HD, 8>(p, causal, st);
+    }
     if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   }
   if constexpr (HD <= 64) return launch_single<HD>(p, causal, st);
