@@ -190,19 +190,26 @@ BENCH_ATTENTION = [("flash_fwd_kernel", 32, 4, 1), ("flash_single_kernel", 64, 2
                    ("flash_fwd_kernel", 128, 8, 1)]
 
 
+# The whole-forward kernel instantiation C1 runs (head_dim 32, causal).
+SMALL_FORWARD_C1 = "_ZN2tk12_GLOBAL__N_120small_forward_kernelILi128ELi128ELi128ELi32ELb1EEEvNS0_9SmallArgsE"
+
+
 def test_hot_kernels_use_no_scratch():
     """A spilled accumulator costs several times the kernel's run time and no
     parity test sees it; the build's resource report must show no scratch for
-    the GEMM, LayerNorm and softmax kernels and the benchmarked attention."""
+    the GEMM, LayerNorm and softmax kernels, the fused QKV + attention kernel
+    and the benchmarked attention and whole-forward instantiations."""
     from tkmi import build as tkbuild
 
     if not tkbuild.RESOURCE_PATH.exists():
         pytest.skip("library not built")
     usage = json.loads(tkbuild.RESOURCE_PATH.read_text())
-    hot = [k for k in usage if any(s in k for s in ("gemm_kernel", "gemm_ln_kernel", "ln_rows_kernel", "softmax_"))]
+    hot = [k for k in usage if any(s in k for s in ("gemm_kernel", "gemm_ln_kernel", "ln_rows_kernel", "softmax_",
+                                                     "qkv_attn_kernel"))]
     assert len(hot) >= 30
     for name, hd, nw, causal in BENCH_ATTENTION:
         hot.append(f"_ZN2tk12_GLOBAL__N_1{len(name)}{name}ILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
+    hot.append(SMALL_FORWARD_C1)
     missing = [k for k in hot if k not in usage]
     assert not missing, missing
     spilled = {k: usage[k]["scratch"] for k in hot if usage[k].get("scratch", 0) > 0}
