@@ -203,14 +203,17 @@ def test_non_prefix_mask_parity(causal, fused):
     assert bool((got[~mask] == 0).all())
 
 
-def test_graphed_forward_replays_match_eager():
+# the layer path; the fused QKV + attention path (S = 64, head_dim 64)
+@pytest.mark.parametrize("shape", [(4, 64, 128, 4, 256, 2, True), (4, 64, 512, 8, 1024, 2, False)],
+                         ids=["layers", "fused_qkv_attention"])
+def test_graphed_forward_replays_match_eager(shape):
     """Whole-forward HIP graph (src/cuda_graphs.py semantics): after the eager
     warm-up calls the graph is captured; every replay -- with eager work and
     synchronisations in between, and with fresh input tensors (copied into the
     captured buffer) -- must equal the eager forward bit for bit."""
     from tkmi.graphs import GraphedTransformer, WARMUP_BEFORE_CAPTURE
 
-    cfg = ob.TransformerConfig(4, 64, 128, 4, 256, 2, True)
+    cfg = ob.TransformerConfig(*shape)
     base = ob.build_model(cfg, seed=11).eval()
     eager = tkmi.OptimizedTransformer(tkmi.TransformerConfig(**cfg.__dict__))
     graphed = GraphedTransformer(tkmi.TransformerConfig(**cfg.__dict__))
