@@ -251,8 +251,12 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     constexpr bool HAS_NEXT = decltype(next_c)::value;
     constexpr bool HAS_PREV = decltype(prev_c)::value;
     const int k0 = kt * kBN;
-    if (kt + 2 < n_kt) copy_k(kt + 2);
-    if (HAS_NEXT) copy_v(kt + 1);
+    // The copies go out from inside the chunk loop (K after chunk 0, V after
+    // chunk 2) rather than here: issued right after the barrier, every wave
+    // of the CU queues its copies at once and stalls on issue before its
+    // first MFMA.  Their LDS slots (tile kt's K, tile kt-2's V) are free
+    // since the previous step's barrier.
+    constexpr int C_K = 0, C_V = NC > 2 ? 2 : NC - 1;
     int kbyte_next = 1;
     if (KMASK && HAS_NEXT) kbyte_next = key_byte(kt + 1);
 
@@ -357,6 +361,8 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
 #pragma unroll
         for (int e = e0; e < e1; ++e) exp_entry(e);
       }
+      if (c == C_K && kt + 2 < n_kt) copy_k(kt + 2);
+      if (c == C_V && HAS_NEXT) copy_v(kt + 1);
       // row max of S(kt+1), spread over the chunks after its last MFMA
       if constexpr (C_MAX < NC) if (HAS_NEXT && c >= C_MAX) {
         const int n = NC - C_MAX;
