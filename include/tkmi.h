@@ -98,7 +98,10 @@ int tk_add_ln_cast(const float *x, const void *y, int y_dtype, const float *w,
  * epilogue TK_EPI_BIAS / TK_EPI_BIAS_GELU: C is f16 (ldc).
  * epilogue TK_EPI_BIAS_RESID: C is f32 (ldc), resid is f32 (ldr), C may
  * equal resid (in-place residual stream update).
- * k must be a multiple of 8 and lda/ldw multiples of 8 (16-byte rows).
+ * Any k >= 0 with lda, ldw >= k; A and W 2-byte aligned.  When k, lda and
+ * ldw are multiples of 8 and A, W 16-byte aligned the operands are read in
+ * 16-byte vectors (the fast path); otherwise by element (odd d_model /
+ * ffn_dim, which the reference's config validation accepts).
  * row_valid / row_mode (TK_EPI_BIAS_RESID only; row_valid nullable, m bytes):
  * an invalid row m is written as resid (TK_ROWS_KEEP_RESID) or 0
  * (TK_ROWS_ZERO, TK_ROWS_ZERO_ALL).
@@ -142,7 +145,12 @@ int tk_gemm_ln_supported(int64_t n);
  * like future keys (src/torch_transformer_benchmark.py:104-107).  A query
  * row with no valid key yields non-finite output (the baseline's NaN row);
  * callers zero such padded rows downstream.
- * head_dim in {16, 32, 64, 128, 256} (tk_attention_supported).
+ * Any head_dim <= 256 (tk_attention_supported) and any element strides;
+ * q/k/v/out 2-byte aligned.  Head dims 16/32/64/128/256 with rows that are
+ * 16-byte vectors (q, k; v too except at 128) and 8-byte vectors (out; v
+ * at 128) take the tuned kernels; every other head dim or view runs on the
+ * tile of the next power of two >= max(head_dim, 16) with element loads and
+ * the head-dim tail read as zeros (src/kernels.py:262-263 pads the same way).
  * Replaces kernels.flash_attention / _flash_attn_fwd_kernel
  * (src/kernels.py:250-294, :137-247) and F.scaled_dot_product_attention
  * (src/optimized.py:615-626).
@@ -155,7 +163,8 @@ int tk_flash_attn_fwd(const tk_half *q, const tk_half *k, const tk_half *v,
                       const uint8_t *key_valid, int64_t key_valid_stride,
                       void *stream);
 
-/* 1 when tk_flash_attn_fwd handles head_dim, else 0.
+/* 1 when tk_flash_attn_fwd handles head_dim, else 0: the reference's rule
+ * next_pow2(max(head_dim, 16)) <= 256, i.e. head_dim <= 256.
  * Replaces kernels.attention_supported (src/kernels.py:96-103). */
 int tk_attention_supported(int64_t head_dim);
 

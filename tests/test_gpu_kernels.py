@@ -243,8 +243,9 @@ def test_gemm_add_layernorm_epilogue(m, n):
 # Attention
 # --------------------------------------------------------------------------- #
 
-ATTN_SHAPES = [  # (B, H, S, hd); the reference's shapes with a supported head_dim
+ATTN_SHAPES = [  # (B, H, S, hd); the reference's shapes (src/test_triton_kernels.py:144-152) first
     (2, 4, 128, 32),
+    (2, 16, 64, 8),     # head_dim 8: the element-load kernel on the 16-wide tile
     (1, 1, 64, 128),
     (2, 4, 96, 32),
     (1, 2, 128, 64),
@@ -374,14 +375,67 @@ def test_flash_attention_key_mask(shape, causal):
 
 
 def test_attention_support_probes():
+    """The reference's rule, next_pow2(max(hd, 16)) <= 256 for fp16 on the GPU
+    (src/kernels.py:96-103); above it the kernel raises."""
     assert ops.attention_supported(64, torch.float16, DEV)
-    assert not ops.attention_supported(8, torch.float16, DEV)
+    assert ops.attention_supported(8, torch.float16, DEV)
+    assert ops.attention_supported(100, torch.float16, DEV)
     assert ops.attention_supported(256, torch.float16, DEV)
+    assert not ops.attention_supported(257, torch.float16, DEV)
     assert not ops.attention_supported(512, torch.float16, DEV)
     assert not ops.attention_supported(64, torch.float32, DEV)
-    q = torch.zeros(1, 1, 8, 8, dtype=torch.float16, device=DEV)
+    q = torch.zeros(1, 1, 8, 264, dtype=torch.float16, device=DEV)
     with pytest.raises(_lib.TkError, match="head_dim"):
         ops.flash_attention(q, q, q, 1.0, True)
+
+
+# Head dims without a tile of their own (the element-load kernel on the next
+# power-of-two tile), on and off the 64-key / 128-row grids.
+ODD_HD_SHAPES = [(1, 2, 64, 1), (2, 3, 100, 24), (1, 2, 333, 40), (2, 2, 130, 100), (1, 2, 257, 200),
+                 (1, 1, 70, 250)]
+
+
+@pytest.mark.parametrize("shape", ODD_HD_SHAPES, ids=lambda s: "b{}h{}s{}d{}".format(*s))
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_flash_attention_any_head_dim(shape, causal):
+    b, h, s, hd = shape
+    q, k, v = _qkv(shape, seed=hd)
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal)
+    assert out.shape == (b, s, h * hd)
+    bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("hd", [24, 64, 128])
+def test_flash_attention_unaligned_views(hd):
+    """q/k/v views whose rows are not 16-byte vectors (a 3-element offset into
+    one buffer, row stride not a multiple of 8) take the element-load path."""
+    b, h, s = 2, 3, 150
+    base = seeded(b * h * s * (hd + 3) + 3, dtype=torch.float16, seed=hd)
+    ref_views = []
+    dev_views = []
+    for i in range(3):
+        flat = base.roll(i * 17)
+        t = flat[3:].view(b, h, s, hd + 3)[..., :hd]
+        ref_views.append(t.contiguous())
+        dev_views.append(flat.to(DEV)[3:].view(b, h, s, hd + 3)[..., :hd])
+    for causal in (True, False):
+        out = ops.flash_attention(*dev_views, hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(*ref_views, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_flash_attention_any_head_dim_key_mask(causal):
+    b, h, s, hd = 2, 2, 150, 48
+    q, k, v = _qkv((b, h, s, hd), seed=48)
+    g = torch.Generator().manual_seed(48)
+    kv = torch.rand(b, s, generator=g) < 0.7
+    kv[:, 0] = True
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, causal, key_valid=kv.to(DEV)).cpu()
+    ref = _attention_ref_keymask(q, k, v, hd ** -0.5, causal, kv)
+    bad, err = or_rule_violations(out, ref)
+    assert bad == 0, err
 
 
 # --------------------------------------------------------------------------- #

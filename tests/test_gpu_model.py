@@ -73,7 +73,9 @@ def test_matches_reference_golden_outputs(name):
     assert res.passed
 
 
-@pytest.mark.parametrize("name,trials", [("C1", 5), ("C2", 5), ("C3", 2)])
+# The harness's accuracy check: 5 trials, inputs seeded 1234 + trial
+# (src/torch_transformer_benchmark.py:382-393), every element of the output.
+@pytest.mark.parametrize("name,trials", [("C1", 5), ("C2", 5)])
 def test_config_parity_full_output(name, trials):
     cfg = CONFIGS[name]
     base, opt = _pair(cfg)
@@ -87,30 +89,87 @@ def test_config_parity_full_output(name, trials):
         assert res.passed
 
 
-def test_config_parity_c4_chunked_oracle():
+_MODEL_CACHE = {}
+
+
+def _cached_pair(name):
+    """One seeded oracle/drop-in pair per large config, shared by its per-trial tests."""
+    if name not in _MODEL_CACHE:
+        _MODEL_CACHE.clear()  # keep one large config's weights resident at a time
+        _MODEL_CACHE[name] = _pair(CONFIGS[name])
+    return _MODEL_CACHE[name]
+
+
+@pytest.mark.parametrize("trial", range(5))
+def test_config_parity_c3(trial):
+    cfg = CONFIGS["C3"]
+    base, opt = _cached_pair("C3")
+    x, mask = ob.generate_random_case(cfg, seed=1234 + trial)
+    with torch.inference_mode():
+        got = opt(x.to(DEV), mask.to(DEV)).cpu()
+        ref = base(x, mask)
+    res = ob.compare_outputs(ref, got)
+    _report(f"C3 trial {trial}", res)
+    assert res.passed
+
+
+@pytest.mark.parametrize("trial", range(5))
+def test_config_parity_c4_chunked_oracle(trial):
+    """Every output element of C4 against the query-chunked oracle (row-exact to
+    the baseline without its 17 GB score tensor)."""
     cfg = CONFIGS["C4"]
-    base, opt = _pair(cfg)
-    x, mask = ob.generate_random_case(cfg, seed=1234)
+    base, opt = _cached_pair("C4")
+    x, mask = ob.generate_random_case(cfg, seed=1234 + trial)
     with torch.inference_mode():
         got = opt(x.to(DEV), mask.to(DEV)).cpu()
         ref = ob.chunked_forward(base, x, q_chunk=2048)
     res = ob.compare_outputs(ref, got)
-    _report("C4 trial 0 (query-chunked oracle)", res)
+    _report(f"C4 trial {trial} (query-chunked oracle)", res)
     assert res.passed
 
 
-def test_config_parity_c5_sampled_rows():
+@pytest.mark.parametrize("trial", range(5))
+def test_config_parity_c5_sampled_rows(trial):
+    """C5 on 512 seeded query rows per sequence (exact for one causal layer)."""
     cfg = CONFIGS["C5"]
-    base, opt = _pair(cfg)
-    x, mask = ob.generate_random_case(cfg, seed=1234)
+    base, opt = _cached_pair("C5")
+    x, mask = ob.generate_random_case(cfg, seed=1234 + trial)
     rows = ob.sample_query_rows(cfg.seq_len, 512, seed=1234)
     with torch.inference_mode():
         got = opt(x.to(DEV), mask.to(DEV))[:, rows.to(DEV)].cpu()
         ref = ob.sampled_rows_forward(base, x, rows, q_chunk=512)
     res = ob.compare_outputs(ref, got)
-    _report("C5 trial 0 (512 sampled query rows)", res)
+    _report(f"C5 trial {trial} (512 sampled query rows)", res)
     assert res.passed
     assert torch.isfinite(got).all()
+
+
+# The reference's accuracy stress: 25 trials under each of two seeds (weights
+# torch.manual_seed(seed), inputs seed + trial; src/run_case.py with
+# --accuracy-trials 25 [--seed 9999], results/pass3-e6-stress-{a,b}.json),
+# which exposed its fp16 failures on appendix case 7 (results/case7-stress-a.json).
+STRESS = {
+    "C1": CONFIGS["C1"],
+    "C2": CONFIGS["C2"],
+    "case7": ob.TransformerConfig(64, 128, 32, 4, 32, 4, True),
+}
+
+
+@pytest.mark.parametrize("seed", [1234, 9999])
+@pytest.mark.parametrize("name", sorted(STRESS))
+def test_accuracy_stress_25_trials(name, seed):
+    cfg = STRESS[name]
+    base, opt = _pair(cfg, seed=seed)
+    worst = 0.0
+    for trial in range(25):
+        x, mask = ob.generate_random_case(cfg, seed=seed + trial)
+        with torch.inference_mode():
+            ref = base(x, mask)
+            got = opt(x.to(DEV), mask.to(DEV)).cpu()
+        res = ob.compare_outputs(ref, got)
+        worst = max(worst, res.max_abs_error)
+        assert res.passed, (trial, res.max_abs_error, res.failed_elements)
+    print(f"stress {name} seed {seed}: 25 trials PASS worst max_abs={worst:.6g}", flush=True)
 
 
 def test_fused_and_unfused_epilogues_agree():
@@ -243,7 +302,9 @@ def test_graphed_forward_replays_match_eager(shape):
 # 8 is appendix case 7's (d_model 32, 4 heads).
 @pytest.mark.parametrize("shape", [(8, 64, 32, 4, 64, 2, True), (2, 96, 96, 4, 192, 2, False),
                                    (2, 160, 192, 4, 256, 1, True), (1, 300, 320, 4, 512, 1, True),
-                                   (2, 130, 800, 4, 256, 1, True)])
+                                   (2, 130, 800, 4, 256, 1, True),
+                                   # S = 64 with head_dim 48 padded to 64: not the fused QKV+attention kernel
+                                   (2, 64, 192, 4, 384, 2, True), (2, 64, 192, 4, 384, 2, False)])
 def test_padded_head_dims(shape):
     cfg = ob.TransformerConfig(*shape)
     base, opt = _pair(cfg)
@@ -254,6 +315,23 @@ def test_padded_head_dims(shape):
         ref = base(x, mask)
     res = ob.compare_outputs(ref, got)
     _report(f"head_dim {opt.head_dim} -> {opt.head_dim_padded}", res)
+    assert res.passed
+
+
+# d_model / ffn_dim that are not multiples of 8 (the reference's validation
+# accepts any positive sizes with d_model % heads == 0): GEMM operand rows are
+# then not 16-byte vectors and take the element-load path.
+@pytest.mark.parametrize("shape", [(2, 50, 100, 4, 100, 2, True), (3, 40, 36, 3, 70, 1, False),
+                                   (2, 130, 256, 4, 300, 1, True), (1, 77, 132, 4, 131, 2, True)])
+def test_unaligned_model_widths(shape):
+    cfg = ob.TransformerConfig(*shape)
+    base, opt = _pair(cfg)
+    x, mask = ob.generate_random_case(cfg, seed=8)
+    with torch.inference_mode():
+        got = opt(x.to(DEV), mask.to(DEV)).cpu()
+        ref = base(x, mask)
+    res = ob.compare_outputs(ref, got)
+    _report(f"d_model {cfg.d_model} ffn {cfg.ffn_dim}", res)
     assert res.passed
 
 

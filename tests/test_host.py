@@ -126,7 +126,9 @@ def test_every_kernel_has_a_launch_stub():
 
 def test_capability_probes():
     lib = _lib.load()
-    assert [lib.tk_attention_supported(h) for h in (8, 16, 32, 64, 128, 256, 512)] == [0, 1, 1, 1, 1, 1, 0]
+    # the reference's rule: next_pow2(max(hd, 16)) <= 256 (src/kernels.py:96-103)
+    hds = (1, 8, 16, 24, 32, 64, 100, 128, 200, 256, 257, 512)
+    assert [lib.tk_attention_supported(h) for h in hds] == [1 if h <= 256 else 0 for h in hds]
     assert [lib.tk_gemm_ln_supported(n) for n in (64, 128, 256, 512, 1024)] == [0, 1, 1, 1, 0]
     # whole-forward kernel: S <= 128, d_model = ffn = 128, heads * padded head_dim = 128
     small = lib.tk_small_forward_supported
@@ -142,7 +144,8 @@ def test_capability_probes():
         ("tk_ln_cast", (None, None, None, None, 1, 4, 64, 1e-5, None, None), _lib.TK_ERR_ARG),
         ("tk_ln_cast", (8, 8, 8, 8, 1, 4, 9000, 1e-5, None, None), _lib.TK_ERR_ARG),
         ("tk_ln_cast", (8, 8, 8, 8, 7, 4, 64, 1e-5, None, None), _lib.TK_ERR_ARG),
-        ("tk_gemm", (16, 12, 16, 12, None, None, 0, 16, 16, 4, 4, 12, 0, None, 0, None), _lib.TK_ERR_ARG),
+        ("tk_gemm", (16, 8, 16, 12, None, None, 0, 16, 16, 4, 4, 12, 0, None, 0, None), _lib.TK_ERR_ARG),  # lda < k
+        ("tk_gemm", (17, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 12, 0, None, 0, None), _lib.TK_ERR_ARG),  # odd A
         ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 9, None, 0, None), _lib.TK_ERR_ARG),
         # a row mask needs the residual epilogue and a valid tk_row_mode
         ("tk_gemm", (16, 16, 16, 16, None, None, 0, 16, 16, 4, 4, 16, 0, 16, 1, None), _lib.TK_ERR_ARG),
@@ -170,9 +173,25 @@ def test_argument_validation_without_gpu(fn, args, code):
 def test_flash_rejects_bad_head_dim_without_gpu():
     lib = _lib.load()
     st = _lib.strides3((0, 0, 0))
-    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 48, st, st, st, st, 1.0, 1, None, 0, None)
+    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 264, st, st, st, st, 1.0, 1, None, 0, None)
     assert status == _lib.TK_ERR_UNSUPPORTED
     assert "head_dim" in lib.tk_last_error_string().decode()
+    status = lib.tk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, -1, st, st, st, st, 1.0, 1, None, 0, None)
+    assert status == _lib.TK_ERR_ARG
+
+
+def test_masked_softmax_checks_key_lengths_against_groups():
+    """key_len is indexed per batch of heads_per_batch score groups; a short or
+    mismatched key_len is rejected before any device read."""
+    import tkmi.ops as ops
+
+    scores = torch.zeros(6, 8, 8)
+    with pytest.raises(ValueError, match="key_len"):
+        ops.masked_softmax(scores, True, key_len=torch.tensor([8, 8], dtype=torch.int32), heads_per_batch=2)
+    with pytest.raises(ValueError, match="key_len"):
+        ops.masked_softmax(scores, True, key_len=torch.tensor([8, 8], dtype=torch.int32), heads_per_batch=4)
+    with pytest.raises(RuntimeError, match="GPU"):  # counts fine: only the device check remains
+        ops.masked_softmax(scores, True, key_len=torch.tensor([8, 8, 8], dtype=torch.int32), heads_per_batch=2)
 
 
 def test_flash_rejects_short_key_mask_stride_without_gpu():

@@ -845,6 +845,181 @@ __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
                                      p.o + b * p.os[0] + h * p.os[1], p.os[2]);
 }
 
+// ---- any head_dim <= 256, any element strides and alignment ----
+// Head dims without a tile of their own (e.g. 8, 24, 100) and q/k/v/out views
+// whose rows are not 16-byte vectors run here, on the tile of the next
+// supported width HDP (the reference pads its head-dim block the same way,
+// src/kernels.py:262-263).  Q, K and V are read element by element with the
+// head-dim tail past hd (and keys past S) filled with zeros, so the padded
+// columns add exact zeros to Q.K^T and produce zero O^T rows that are never
+// stored; no padded copy of any operand is made.  Four waves of 32 query rows,
+// one 64-key tile at a time through registers into the flash_dma_body LDS
+// layouts (K chunk-swizzled, V for the transposed reads), exact online
+// softmax (the running max moves with every tile), O stored element-wise.
+template <int HDP, bool CAUSAL, bool KMASK>
+__global__ __launch_bounds__(256) void flash_generic_kernel(AttnArgs p, int hd) {
+  constexpr int NW = 4, BM = 32 * NW, NT = 64 * NW;
+  constexpr int RB = HDP * 2;              // K / V tile row bytes
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;
+  constexpr int DB = (HDP + 31) / 32;
+  constexpr int KSTEPS = HDP / 16;
+  constexpr int NP = 4 * DB;
+  constexpr int LOADS = (kBN * CPR + NT - 1) / NT;  // 16-byte chunks per thread per tile
+  __shared__ __attribute__((aligned(16))) char smem[2 * TILE];
+  char* ks_ = smem;
+  char* vs_ = smem + TILE;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = p.B * p.H;
+  const int n_qt = (p.S + BM - 1) / BM;
+  const int qt = CAUSAL ? (n_qt - 1 - (int)blockIdx.x / BH) : (int)blockIdx.x / BH;
+  const int bh = blockIdx.x % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = qt * BM;
+  const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
+  const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
+  const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kvs : nullptr;
+  const int my_row = q0 + wave * 32 + (lane & 31);
+  const int g = lane >> 5;
+
+  f16x8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int col = kk * 16 + g * 8 + e;
+      qf[kk][e] = (my_row < p.S && col < hd) ? qb[(int64_t)my_row * p.qs[2] + col] : (f16)0;
+    }
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[d][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  int v_rd[2][DB];
+  {
+    const int tq = lane >> 4, ts = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
+        const int col = 32 * d + (HDP >= 32 ? 16 * (tq & 1) : 0) + 4 * (ts & 3);
+        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
+      }
+  }
+  const bool d_ok = HDP % 32 == 0 || (lane & 31) < HDP;
+
+  const int kv_end = CAUSAL ? min(p.S, q0 + BM) : p.S;
+  const int n_kt = (kv_end + kBN - 1) / kBN;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int k0 = kt * kBN;
+    __syncthreads();  // the previous tile's operands are no longer read
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int idx = tid + i * NT;
+      if (LOADS * NT == kBN * CPR || idx < kBN * CPR) {
+        const int row = idx / CPR, ch = idx % CPR;
+        const int key = k0 + row;
+        f16x8 kv8, vv8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int col = ch * 8 + e;
+          const bool in = key < p.S && col < hd;
+          kv8[e] = in ? kb[(int64_t)key * p.ks[2] + col] : (f16)0;
+          vv8[e] = in ? vb[(int64_t)key * p.vs[2] + col] : (f16)0;
+        }
+        *reinterpret_cast<f16x8*>(ks_ + swz_off<RB>(row, ch)) = kv8;
+        *reinterpret_cast<f16x8*>(vs_ + row * RB + ((ch ^ vswz<RB>(row)) << 4)) = vv8;
+      }
+    }
+    const uint64_t kbits = KMASK ? (uint64_t)__ballot(kvb[min(k0 + lane, p.S - 1)] != 0) >> (4 * g) : 0ull;
+    __syncthreads();
+
+    f32x16 s[2];
+#pragma unroll
+    for (int c = 0; c < 2 * KSTEPS; ++c) {
+      const int kb2 = c / KSTEPS, kk = c % KSTEPS;
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>(kb2 * 32 + (lane & 31), 2 * kk + g));
+      s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kk], kk == 0 ? f32x16{} : s[kb2], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+        const int key = k0 + j + 4 * g;
+        if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kbits >> j) & 1) == 0)) s[kb2][r] = -INFINITY;
+        mx = fmaxf(mx, s[kb2][r]);
+      }
+    mx = pair_max(mx);
+    const float cs = p.scale_log2;
+    const float m_new = fmaxf(m_run, mx * cs);
+    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+    f16x8 pf[4];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use));
+      const f16 ph = (f16)pv;
+      pf[e >> 3][e & 7] = ph;
+      l_run += (float)ph;
+    }
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      const int t = c / DB, d = c % DB;
+      const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
+      const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
+      const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
+      f16x8 vf = __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2, 3,
+                                         4, 5, 6, 7);
+      if (!d_ok) vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      acc_o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], acc_o[d], 0, 0, 0);
+    }
+  }
+
+  const float inv = 1.0f / pair_sum(l_run);
+  if (my_row < p.S) {
+    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = d * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (dd < hd) ob[dd] = (f16)(acc_o[d][r] * inv);
+      }
+  }
+}
+
+template <int HDP>
+int launch_generic(const AttnArgs& p, int hd, bool causal, hipStream_t st) {
+  const int64_t grid = (int64_t)((p.S + 127) / 128) * p.B * p.H;
+  const dim3 g((unsigned)grid), blk(256);
+  const bool km = p.kv != nullptr;
+  if (causal && km)
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, true>), g, blk, 0, st, p, hd);
+  else if (causal)
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, false>), g, blk, 0, st, p, hd);
+  else if (km)
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, true>), g, blk, 0, st, p, hd);
+  else
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, false>), g, blk, 0, st, p, hd);
+  return check_launch("tk_flash_attn_fwd");
+}
+
 // Four-wave workgroups at head_dim <= 64 ask for two waves per SIMD (two
 // workgroups per CU): left alone the compiler spends 280-370 registers on
 // them (one wave per SIMD).  With two independent workgroups per CU one
@@ -923,9 +1098,19 @@ int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 
 using namespace tk;
 
-extern "C" int tk_attention_supported(int64_t head_dim) {
-  return head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+// The reference's rule (src/kernels.py:96-103): the head-dim block, the next
+// power of two >= max(head_dim, 16), must be at most 256.
+extern "C" int tk_attention_supported(int64_t head_dim) { return head_dim <= 256; }
+
+namespace {
+// Head dims with a tile of their own, whose views take the vector paths.
+bool native_head_dim(int64_t hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256; }
+int64_t head_dim_block(int64_t hd) {
+  int64_t b = 16;
+  while (b < hd) b *= 2;
+  return b;
 }
+}  // namespace
 
 extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_half* v, tk_half* out,
                                  int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
@@ -935,20 +1120,18 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
                                  void* stream) {
   TK_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && o_strides, TK_ERR_ARG,
              "tk_flash_attn_fwd: null pointer");
+  TK_REQUIRE(head_dim >= 0, TK_ERR_ARG, "tk_flash_attn_fwd: head_dim=%lld < 0", (long long)head_dim);
   TK_REQUIRE(tk_attention_supported(head_dim), TK_ERR_UNSUPPORTED,
-             "tk_flash_attn_fwd: head_dim=%lld not in {16, 32, 64, 128, 256}", (long long)head_dim);
+             "tk_flash_attn_fwd: head_dim=%lld above 256", (long long)head_dim);
   TK_REQUIRE(batch >= 0 && heads >= 0 && seq >= 0 && batch * heads < (1ll << 31) &&
                  seq < (1ll << 30),
              TK_ERR_ARG, "tk_flash_attn_fwd: bad sizes");
   auto al = [](const void* ptr, uintptr_t a) { return ((uintptr_t)ptr % a) == 0; };
-  TK_REQUIRE(al(q, 16) && al(k, 16) && al(v, 8) && al(out, 8), TK_ERR_ARG,
-             "tk_flash_attn_fwd: q/k need 16-byte, v/out 8-byte alignment");
-  for (int i = 0; i < 3; ++i) {
-    TK_REQUIRE(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 4 == 0 &&
-                   o_strides[i] % 4 == 0,
-               TK_ERR_ARG, "tk_flash_attn_fwd: strides must keep 16-byte (q,k) / 8-byte (v,o) rows");
-  }
-  if (batch == 0 || heads == 0 || seq == 0) return TK_OK;
+  TK_REQUIRE(al(q, 2) && al(k, 2) && al(v, 2) && al(out, 2), TK_ERR_ARG,
+             "tk_flash_attn_fwd: q/k/v/out must be 2-byte aligned");
+  TK_REQUIRE(key_valid == nullptr || key_valid_stride >= seq, TK_ERR_ARG,
+             "tk_flash_attn_fwd: key_valid_stride=%lld < seq=%lld", (long long)key_valid_stride, (long long)seq);
+  if (batch == 0 || heads == 0 || seq == 0 || head_dim == 0) return TK_OK;
   AttnArgs p{};
   p.q = reinterpret_cast<const f16*>(q);
   p.k = reinterpret_cast<const f16*>(k);
@@ -957,19 +1140,34 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
   for (int i = 0; i < 3; ++i) {
     p.qs[i] = q_strides[i]; p.ks[i] = k_strides[i]; p.vs[i] = v_strides[i]; p.os[i] = o_strides[i];
   }
-  TK_REQUIRE(key_valid == nullptr || key_valid_stride >= seq, TK_ERR_ARG,
-             "tk_flash_attn_fwd: key_valid_stride=%lld < seq=%lld", (long long)key_valid_stride, (long long)seq);
   p.kv = key_valid;
   p.kvs = key_valid_stride;
   p.B = (int)batch; p.H = (int)heads; p.S = (int)seq;
   p.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);
   const bool c = causal != 0;
-  switch (head_dim) {
-    case 16: return dispatch_flash<16>(p, c, st);
-    case 32: return dispatch_flash<32>(p, c, st);
-    case 64: return dispatch_flash<64>(p, c, st);
-    case 128: return dispatch_flash<128>(p, c, st);
-    default: return dispatch_flash<256>(p, c, st);
+  // Vector paths: q, k rows 16-byte vectors (register / LDS-DMA copies); v
+  // rows 16-byte vectors where V is DMA-copied (every head dim but 128, whose
+  // body loads V rows 8 bytes at a time); out rows 8-byte vectors.
+  bool vec = native_head_dim(head_dim) && al(q, 16) && al(k, 16) && al(v, head_dim == 128 ? 8 : 16) && al(out, 8);
+  for (int i = 0; i < 3; ++i)
+    vec = vec && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % (head_dim == 128 ? 4 : 8) == 0 &&
+          o_strides[i] % 4 == 0;
+  if (vec) {
+    switch (head_dim) {
+      case 16: return dispatch_flash<16>(p, c, st);
+      case 32: return dispatch_flash<32>(p, c, st);
+      case 64: return dispatch_flash<64>(p, c, st);
+      case 128: return dispatch_flash<128>(p, c, st);
+      default: return dispatch_flash<256>(p, c, st);
+    }
+  }
+  const int hd = (int)head_dim;
+  switch (head_dim_block(head_dim)) {
+    case 16: return launch_generic<16>(p, hd, c, st);
+    case 32: return launch_generic<32>(p, hd, c, st);
+    case 64: return launch_generic<64>(p, hd, c, st);
+    case 128: return launch_generic<128>(p, hd, c, st);
+    default: return launch_generic<256>(p, hd, c, st);
   }
 }

@@ -44,6 +44,7 @@ struct GemmArgs {
   float eps;
   bool vec;     // output rows admit 4-wide vector stores
   bool bias16;  // bias is 16-byte aligned
+  bool kvec;    // K, lda, ldw multiples of 8 and A, W 16-byte aligned: 16-byte operand loads
   int64_t w_gstride;  // grouped W rows (Mainloop WG > 0): group stride in rows
 };
 
@@ -295,20 +296,32 @@ struct Mainloop {
         const int idx = tid + i * NT;
         const int row = idx / CPR, ch = idx % CPR;
         const int gm = m0 + row, gk = k0 + ch * 8;
-        if (gm < p.M && gk < p.K)
-          ra[i] = *reinterpret_cast<const f16x8*>(p.a + (int64_t)gm * p.lda + gk);
-        else
-          ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        ra[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (gm < p.M && gk < p.K) {
+          const f16* src = p.a + (int64_t)gm * p.lda + gk;
+          if (p.kvec) {
+            ra[i] = *reinterpret_cast<const f16x8*>(src);
+          } else {  // rows not 16-byte vectors along K: element loads, zero past K
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ra[i][e] = gk + e < p.K ? src[e] : (f16)0;
+          }
+        }
       }
 #pragma unroll
       for (int i = 0; i < W_LOADS; ++i) {
         const int idx = tid + i * NT;
         const int row = idx / CPR, ch = idx % CPR;
         const int gn = n0 + row, gk = k0 + ch * 8;
-        if (gn < p.N && gk < p.K)
-          rw[i] = *reinterpret_cast<const f16x8*>(p.w + (int64_t)gn * p.ldw + gk);
-        else
-          rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        rw[i] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (gn < p.N && gk < p.K) {
+          const f16* src = p.w + (int64_t)gn * p.ldw + gk;
+          if (p.kvec) {
+            rw[i] = *reinterpret_cast<const f16x8*>(src);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rw[i][e] = gk + e < p.K ? src[e] : (f16)0;
+          }
+        }
       }
     };
     auto land = [&](int stage) {
@@ -762,8 +775,8 @@ __global__ __launch_bounds__(T::NT) void gemm_ln_kernel(GemmArgs p) {
 template <class T, int EPI>
 int launch_gemm(const GemmArgs& p, hipStream_t st) {
   const int64_t tiles = (int64_t)((p.M + T::BM - 1) / T::BM) * ((p.N + T::BN - 1) / T::BN);
-  // The direct global->LDS copy needs whole K tiles.
-  if (p.K % T::BK == 0) {
+  // The direct global->LDS copy needs whole K tiles of 16-byte row chunks.
+  if (p.K % T::BK == 0 && p.kvec) {
     hipLaunchKernelGGL((gemm_kernel<T, EPI, true>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
   } else {
     hipLaunchKernelGGL((gemm_kernel<T, EPI, false>), dim3((unsigned)tiles), dim3(T::NT), 0, st, p);
@@ -799,7 +812,7 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
 template <class T>
 int launch_gemm_ln(const GemmArgs& p, bool h_half, hipStream_t st) {
   const dim3 grid((unsigned)((p.M + T::BM - 1) / T::BM)), block(T::NT);
-  if (p.K % T::BK == 0) {
+  if (p.K % T::BK == 0 && p.kvec) {
     if (h_half) hipLaunchKernelGGL((gemm_ln_kernel<T, true, true>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((gemm_ln_kernel<T, false, true>), grid, block, 0, st, p);
   } else {
@@ -902,10 +915,10 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
   TK_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
              TK_ERR_ARG, "tk_gemm: bad sizes m=%lld n=%lld k=%lld", (long long)m, (long long)n,
              (long long)k);
-  TK_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k, TK_ERR_ARG,
-             "tk_gemm: k=%lld lda=%lld ldw=%lld must be multiples of 8 with ld >= k", (long long)k,
-             (long long)lda, (long long)ldw);
-  TK_REQUIRE(aligned16(a) && aligned16(w), TK_ERR_ARG, "tk_gemm: A and W must be 16-byte aligned");
+  TK_REQUIRE(lda >= k && ldw >= k, TK_ERR_ARG, "tk_gemm: lda=%lld ldw=%lld must be >= k=%lld",
+             (long long)lda, (long long)ldw, (long long)k);
+  TK_REQUIRE(((uintptr_t)a & 1) == 0 && ((uintptr_t)w & 1) == 0, TK_ERR_ARG,
+             "tk_gemm: A and W must be 2-byte aligned");
   TK_REQUIRE(epilogue == TK_EPI_BIAS || epilogue == TK_EPI_BIAS_GELU || epilogue == TK_EPI_BIAS_RESID,
              TK_ERR_ARG, "tk_gemm: bad epilogue %d", epilogue);
   TK_REQUIRE(ldc >= n, TK_ERR_ARG, "tk_gemm: ldc=%lld < n=%lld", (long long)ldc, (long long)n);
@@ -925,6 +938,7 @@ extern "C" int tk_gemm(const tk_half* a, int64_t lda, const tk_half* w, int64_t 
   else
     p.vec = aligned16(c) && ldc % 8 == 0;
   p.bias16 = bias != nullptr && aligned16(bias);
+  p.kvec = k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && aligned16(a) && aligned16(w);
   p.a = reinterpret_cast<const f16*>(a);
   p.w = reinterpret_cast<const f16*>(w);
   p.bias = bias;
@@ -953,10 +967,10 @@ extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half*
              "tk_gemm_bias_add_ln: row width n=%lld not in {128, 256, 512}", (long long)n);
   TK_REQUIRE(m >= 0 && m < (1ll << 31) && k >= 0 && k < (1ll << 31), TK_ERR_ARG,
              "tk_gemm_bias_add_ln: bad sizes");
-  TK_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k, TK_ERR_ARG,
-             "tk_gemm_bias_add_ln: k, lda, ldw must be multiples of 8 with ld >= k");
+  TK_REQUIRE(lda >= k && ldw >= k, TK_ERR_ARG, "tk_gemm_bias_add_ln: lda, ldw must be >= k");
   TK_REQUIRE(h_dtype == TK_F16 || h_dtype == TK_F32, TK_ERR_ARG, "tk_gemm_bias_add_ln: bad h_dtype");
-  TK_REQUIRE(aligned16(a) && aligned16(w) && aligned16(resid) && aligned16(ln_w) && aligned16(ln_b) &&
+  TK_REQUIRE(((uintptr_t)a & 1) == 0 && ((uintptr_t)w & 1) == 0 && aligned16(resid) && aligned16(ln_w) &&
+                 aligned16(ln_b) &&
                  aligned16(h_out) && (sum_out == nullptr || aligned16(sum_out)) &&
                  (bias == nullptr || aligned16(bias)),
              TK_ERR_ARG, "tk_gemm_bias_add_ln: buffers must be 16-byte aligned");
@@ -974,6 +988,7 @@ extern "C" int tk_gemm_bias_add_ln(const tk_half* a, int64_t lda, const tk_half*
   p.ln_w = ln_w;
   p.ln_b = ln_b;
   p.sum_out = sum_out;
+  p.kvec = k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && aligned16(a) && aligned16(w);
   p.lda = lda; p.ldw = ldw; p.ldr = n; p.ldc = n;
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
   p.eps = eps;

@@ -280,7 +280,9 @@ class OptimizedTransformer(BaselineTransformer):
 
         resid = torch.empty((t, d), dtype=torch.float32, device=dev)
         h = torch.empty((t, d), dtype=torch.float16, device=dev)
-        fused_qa = (mask is None and self.settings.qkv_attention
+        # The fused QKV + attention kernel reads h as [T, heads * head_dim]:
+        # only for unpadded head dims (h is [T, d_model]).
+        fused_qa = (mask is None and self.settings.qkv_attention and hd == self.head_dim
                     and ops.qkv_attention_supported(bsz, seq, nh, hd))
         qkv = None if fused_qa else torch.empty((t, 3 * dp), dtype=torch.float16, device=dev)
         ctx = torch.empty((t, dp), dtype=torch.float16, device=dev)

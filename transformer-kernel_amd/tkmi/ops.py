@@ -342,13 +342,24 @@ def small_forward(x, out, stacked: dict, final: tuple, n1_eps: float, n2_eps: fl
 
 
 def masked_softmax(scores, causal: bool, key_len=None, heads_per_batch: int = 1):
-    """fp16 softmax of fp32 ``scores [..., S, S]`` with causal / per-batch key-length masking."""
-    _require_cuda(scores)
-    if scores.dtype != torch.float32 or scores.shape[-1] != scores.shape[-2]:
+    """fp16 softmax of fp32 ``scores [..., S, S]`` with causal / per-batch key-length masking.
+
+    ``key_len`` (optional, one int per batch): the kernel reads the length of
+    score group g at ``key_len[g // heads_per_batch]``, so the groups must be
+    whole batches of ``heads_per_batch`` heads and ``key_len`` must hold one
+    entry per batch.
+    """
+    if scores.dtype != torch.float32 or scores.dim() < 2 or scores.shape[-1] != scores.shape[-2]:
         raise ValueError("scores must be fp32 [..., S, S]")
+    s = scores.shape[-1]
+    groups = scores.numel() // (s * s) if s else 0
+    if key_len is not None:
+        hpb = int(heads_per_batch)
+        if hpb < 1 or groups % hpb != 0 or key_len.numel() * hpb != groups:
+            raise ValueError(f"key_len needs one entry per batch of {heads_per_batch} heads: {groups} score groups, "
+                             f"{key_len.numel()} lengths")
+    _require_cuda(scores)
     sc = scores.contiguous()
-    s = sc.shape[-1]
-    groups = sc.numel() // (s * s) if s else 0
     probs = torch.empty(sc.shape, dtype=torch.float16, device=sc.device)
     kl = None
     if key_len is not None:
