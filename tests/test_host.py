@@ -228,6 +228,12 @@ def test_hot_kernels_use_no_scratch():
     assert len(hot) >= 30
     for name, hd, nw, causal in BENCH_ATTENTION:
         hot.append(f"_ZN2tk12_GLOBAL__N_1{len(name)}{name}ILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
+    # every head_dim-128 instantiation, the padding-mask (key-validity) ones included:
+    # the harness's --padding-ratio path at C4-like shapes
+    hd128 = [k for k in usage if "flash_fwd_kernelILi128E" in k]
+    assert len(hd128) == 12
+    hot += hd128
+    hot += [k for k in usage if "flash_generic_kernel" in k]
     hot.append(SMALL_FORWARD_C1)
     missing = [k for k in hot if k not in usage]
     assert not missing, missing

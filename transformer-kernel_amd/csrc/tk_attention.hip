@@ -774,6 +774,289 @@ __device__ __forceinline__ void flash_vreg_body(const AttnArgs& p) {
   }
 }
 
+// ---- head_dim 128: K and V by LDS-DMA rings, P.V deferred one step ----
+// Step t computes S^T(t) = K(t).Q^T, then runs the O^T MFMAs of tile t-1
+// (P(t-1) from the previous step, V(t-1) by transposed LDS reads) between
+// the exponentials of tile t.  No scores are computed ahead, so one score
+// tile and two fp16 P tiles are live beside the 128-wide O accumulator and
+// the Q fragments (about 200 registers: two waves per SIMD fit without
+// spilling).  At head_dim 128 a step's P.V MFMAs (16 per wave, 512 cycles)
+// cover its exponential work, so the only MFMA-idle phase of a wave is the
+// row max between its S^T and P.V MFMAs, which the other wave of the SIMD
+// fills.  K and V rings of three 16 KB slots: the copies of K(t+2) and
+// V(t+1) are issued during step t and must land by the end of step t+1, so
+// each copy has a whole step of slack beyond the step that issues it; the
+// barrier at the end of a step waits only for the previous step's copies.
+template <int HD, int NW, bool CAUSAL, bool KMASK>
+__device__ __forceinline__ void flash_ring_body(const AttnArgs& p) {
+  constexpr int BM = 32 * NW;
+  constexpr int RB = HD * 2;               // K / V tile row bytes
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;           // bytes per K or V tile
+  constexpr int COPIES = TILE / 1024;      // 1 KB wave copies per tile
+  constexpr int CPW = COPIES / NW;         // copies per wave per tile
+  constexpr int RPC = 1024 / RB;           // tile rows per copy
+  constexpr int DB = HD / 32;              // 32-row blocks of the O^T accumulator
+  constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
+  constexpr int NS = 2 * KSTEPS;           // S^T MFMAs per tile
+  constexpr int NP = 4 * DB;               // O^T MFMAs per tile
+  constexpr int SL = 3;                    // slots per ring
+  static_assert(HD % 32 == 0 && COPIES % NW == 0, "whole copies per wave");
+  static_assert(32 % NP == 0 || NP % 32 == 0, "exponentials spread evenly over the P.V MFMAs");
+
+  __shared__ __attribute__((aligned(16))) char smem[2 * SL * TILE];
+  const uint32_t lds_base = (uint32_t)(size_t)(lds_char*)smem;
+  auto kslot = [&](int i) { return smem + i * TILE; };
+  auto vslot = [&](int i) { return smem + (SL + i) * TILE; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = p.B * p.H;
+  const int n_qt = (p.S + BM - 1) / BM;
+  // Heaviest (last) query tiles first; bh fastest so that a head's tiles
+  // stay on one XCD (hardware ids are dealt round-robin over 8 XCDs).
+  const int id = blockIdx.x;
+  const int qt = CAUSAL ? (n_qt - 1 - id / BH) : id / BH;
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = qt * BM;
+
+  const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
+  const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
+  const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kvs : nullptr;
+
+  const int my_row = q0 + wave * 32 + (lane & 31);
+  const int g = lane >> 5;
+  const int wave_row_min = q0 + wave * 32;
+
+  f16x8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if (my_row < p.S)
+      qf[kk] = *reinterpret_cast<const f16x8*>(qb + (int64_t)my_row * p.qs[2] + kk * 16 + g * 8);
+    else
+      qf[kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  wait_copies();  // Q is in registers before any copy is issued
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[d][r] = 0.f;
+  float m_run = -INFINITY;  // running max of scale*log2e*s
+  float l_run = 0.f;        // lane-partial running sum (this lane's keys)
+
+  const int kv_end = CAUSAL ? min(p.S, q0 + BM) : p.S;
+  const int n_kt = (kv_end + kBN - 1) / kBN;
+
+  // ---- copies (the layouts of flash_dma_body) ----
+  int c_row[CPW], k_col[CPW], v_col[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int ci = wave + i * NW;
+    const int row = ci * RPC + lane / CPR;
+    const int phys = lane % CPR;
+    c_row[i] = row;
+    k_col[i] = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
+    v_col[i] = (phys ^ vswz<RB>(row)) * 8;
+  }
+  auto copy_tile = [&](const f16* base, int64_t rs, const int (&col)[CPW], int j, uint32_t dst) {
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      // rows past S re-read row S-1 (finite; masked or multiplied by P = 0)
+      const int key = min(j * kBN + c_row[i], p.S - 1);
+      dma16(base + (int64_t)key * rs + col[i], dst + (wave + i * NW) * 1024);
+    }
+  };
+  auto copy_k = [&](int j) { copy_tile(kb, p.ks[2], k_col, j, lds_base + (j % SL) * TILE); };
+  auto copy_v = [&](int j) { copy_tile(vb, p.vs[2], v_col, j, lds_base + (SL + j % SL) * TILE); };
+
+  // ---- operand reads ----
+  // S^T MFMA c: key block c & 1, k-step c >> 1 (the two accumulation chains alternate)
+  auto read_k = [&](const char* ks_, int c) {
+    return *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>((c & 1) * 32 + (lane & 31), 2 * (c >> 1) + g));
+  };
+  int v_rd[2][DB];
+  {
+    const int tq = lane >> 4, ts = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
+        const int col = 32 * d + 16 * (tq & 1) + 4 * (ts & 3);
+        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
+      }
+  }
+  auto read_v = [&](const char* vs_, int c) -> f16x8 {
+    const int t = c / DB, d = c % DB;
+    const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
+    const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
+    const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
+    return __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2, 3, 4, 5,
+                                   6, 7);
+  };
+
+  auto key_byte = [&](int kt) { return KMASK ? (int)kvb[min(kt * kBN + lane, p.S - 1)] : 1; };
+  uint64_t kbits_cur = KMASK ? (uint64_t)__ballot(key_byte(0) != 0) : 0ull;  // bit j: key j of the tile valid
+  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
+  constexpr int RA = 3;  // operand reads run this many MFMAs ahead of their use
+
+  // One step: S^T(kt); row max; P.V of tile kt-1 interleaved with the
+  // exponentials of tile kt; copies of K(kt+2) and V(kt+1).  Accumulator
+  // entry r of block kb2 is key k0 + 32*kb2 + 8*(r/4) + 4*g + r%4.
+  auto step = [&](int kt, f16x8 (&p_cur)[4], const f16x8 (&p_prev)[4], auto prev_c) {
+    constexpr bool HAS_PREV = decltype(prev_c)::value;
+    const int k0 = kt * kBN;
+    const bool cp_k = kt + 2 < n_kt, cp_v = kt + 1 < n_kt;
+    // the next tile's key-validity byte: loaded here, turned into bits after
+    // the step's copy wait (its use would otherwise wait for the copies)
+    int kbyte_next = 1;
+    if (KMASK && cp_v) kbyte_next = key_byte(kt + 1);
+
+    // ---- S^T(kt) = K(kt) . Q^T; the step's copies go out behind the first MFMAs ----
+    const char* ks_ = kslot(kt % SL);
+    f32x16 s[2];
+    f16x8 kfr[NS];
+#pragma unroll
+    for (int c = 0; c < RA; ++c) kfr[c] = read_k(ks_, c);
+#pragma unroll
+    for (int c = 0; c < NS; ++c) {
+      if (c + RA < NS) kfr[c + RA] = read_k(ks_, c + RA);
+      const int kb2 = c & 1, kk = c >> 1;
+      s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr[c], qf[kk], kk == 0 ? f32x16{} : s[kb2], 0, 0, 0);
+      if (c == NS / 4 && cp_k) copy_k(kt + 2);
+      if (c == NS / 2 && cp_v) copy_v(kt + 1);
+    }
+
+    // ---- mask and row max ----
+    float mx = -INFINITY;
+    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
+    if (need_mask) {
+      // bit j of kbits: key k0 + 4*g + j is valid
+      const uint64_t kbits = kbits_cur >> (4 * g);
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+          const int key = k0 + j + 4 * g;
+          if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kbits >> j) & 1) == 0))
+            s[kb2][r] = -INFINITY;
+          mx = fmaxf(mx, s[kb2][r]);
+        }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 32; ++e) mx = fmaxf(mx, s[e >> 4][e & 15]);
+    }
+    mx = pair_max(mx);
+    const float cs = p.scale_log2;
+    const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
+    // Lazy rescale (as flash_dma_body): the reference max moves only when a
+    // row of the wave has grown by more than 2^8 over it.  O is rescaled
+    // after the deferred P.V MFMAs have added tile kt-1 at the old reference.
+    const bool rescale = __any(m_tile > m_run + 8.0f);
+    float alpha = 1.0f;
+    if (rescale) {
+      const float m_new = fmaxf(m_run, m_tile);
+      alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+
+    // ---- P.V(kt-1) MFMAs interleaved with the exponentials of tile kt ----
+    const char* vs_p = vslot((kt + SL - 1) % SL);
+    f16x8 vfr[NP];
+    if (HAS_PREV) {
+#pragma unroll
+      for (int c = 0; c < RA; ++c) vfr[c] = read_v(vs_p, c);
+    }
+    float ls = 0.f;
+    auto exp_pair = [&](int e) {  // entries e, e+1 (e even)
+      const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use)),
+                        (f16)__builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use))};
+      p_cur[e >> 3][e & 7] = hp[0];
+      p_cur[e >> 3][(e & 7) + 1] = hp[1];
+      ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+    };
+    constexpr int EPM = 32 / NP;  // exponentials per P.V MFMA
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      if (HAS_PREV) {
+        if (c + RA < NP) vfr[c + RA] = read_v(vs_p, c + RA);
+        acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vfr[c], p_prev[c / DB], acc_o[c % DB], 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = c * EPM; e < (c + 1) * EPM; e += 2) exp_pair(e);
+    }
+    l_run += ls;
+    if (rescale) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+    }
+    // ---- K(kt+1) and V(kt) (issued last step) land; this step's copies may stay in flight ----
+    __builtin_amdgcn_sched_barrier(0);
+    if (cp_k) wait_vmcnt<2 * CPW>();
+    else if (cp_v) wait_vmcnt<CPW>();
+    else wait_vmcnt<0>();
+    if (KMASK && cp_v) kbits_cur = (uint64_t)__ballot(kbyte_next != 0);
+    lds_barrier();
+  };
+
+  // ---- prologue: K(0), K(1), V(0) resident ----
+  copy_k(0);
+  if (n_kt > 1) copy_k(1);
+  copy_v(0);
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  const BoolC<true> T{};
+  const BoolC<false> F{};
+  f16x8 pf_a[4], pf_b[4];
+  step(0, pf_a, pf_b, F);
+  int kt = 1;
+  // two steps per iteration: the P buffers swap roles without register copies
+  for (; kt + 1 < n_kt; kt += 2) {
+    step(kt, pf_b, pf_a, T);
+    step(kt + 1, pf_a, pf_b, T);
+  }
+  // ---- O^T += V^T . P^T of the last tile ----
+  auto pv_last = [&](const f16x8(&pl)[4]) {
+    const char* vs_l = vslot((n_kt - 1) % SL);
+#pragma unroll
+    for (int c = 0; c < NP; ++c)
+      acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(vs_l, c), pl[c / DB], acc_o[c % DB], 0, 0, 0);
+  };
+  if (kt < n_kt) {
+    step(kt, pf_b, pf_a, T);
+    pv_last(pf_b);
+  } else {
+    pv_last(pf_a);
+  }
+
+  // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
+  l_run = pair_sum(l_run);
+  const float inv = 1.0f / l_run;
+  if (my_row < p.S) {
+    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int dd = d * 32 + 8 * q + 4 * g;
+        f16x4 t = {(f16)(acc_o[d][4 * q] * inv), (f16)(acc_o[d][4 * q + 1] * inv),
+                   (f16)(acc_o[d][4 * q + 2] * inv), (f16)(acc_o[d][4 * q + 3] * inv)};
+        *reinterpret_cast<f16x4*>(ob + dd) = t;
+      }
+  }
+}
+
 // ---- one key tile (S <= 64, head_dim <= 64) ----
 // Short sequences are latency-bound (the reference's B256 S64 config runs
 // 2048 heads of one tile each): a workgroup loads Q, one K and one V tile
@@ -1029,8 +1312,17 @@ int launch_generic(const AttnArgs& p, int hd, bool causal, hipStream_t st) {
 // causal 129 -> 118 us, b2 s32768 causal 5.81 -> 5.73 ms).
 template <int HD, int NW, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64, (NW <= 4 && HD <= 64) ? 2 : 1) void flash_fwd_kernel(AttnArgs p) {
-  if constexpr (HD == 128) flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
-  else flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
+  // head_dim 128: causal launches take the DMA-ring body (C4 shape b4 s8192:
+  // 1263-1295 -> 1180-1199 us in alternating same-box runs); without the
+  // causal diagonal the register body stays (its ring build spills ~100 B
+  // there: b2 s4096 non-causal 318-340 vs 354 us).
+  if constexpr (HD == 128 && CAUSAL) {
+    flash_ring_body<HD, NW, CAUSAL, KMASK>(p);
+  } else if constexpr (HD == 128) {
+    flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
+  } else {
+    flash_dma_body<HD, NW, CAUSAL, KMASK>(p);
+  }
 }
 template <int HD, int NW, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64, 4) void flash_single_kernel(AttnArgs p) {

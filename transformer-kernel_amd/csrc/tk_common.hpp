@@ -60,6 +60,27 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
       : "memory");
 }
 
+// s_waitcnt with vmcnt <= N, other counters unconstrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the memory fence of __syncthreads() (which
+// waits for every outstanding vector-memory op, i.e. drains all in-flight
+// tile copies).  The empty asm statements keep the compiler from moving LDS
+// accesses across it; the direct-copy loop orders the copies itself with
+// wait_vmcnt, and every fragment read has completed before the MFMA that
+// consumes it was issued.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+
 // ---------------------------------------------------------------- errors --
 // Per-thread status text behind tk_last_error_string().
 void set_error(const char* fmt, ...);

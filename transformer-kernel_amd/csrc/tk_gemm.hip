@@ -61,26 +61,6 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * 32 + ((chunk ^ ((row >> 2) & 3)) << 3);
 }
 
-// s_waitcnt with vmcnt <= N, other counters unconstrained (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier without the memory fence of __syncthreads() (which
-// waits for every outstanding vector-memory op, i.e. drains all in-flight
-// tile copies).  The empty asm statements keep the compiler from moving LDS
-// accesses across it; the direct-copy loop orders the copies itself with
-// wait_vmcnt, and every fragment read has completed before the MFMA that
-// consumes it was issued.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Maps the hardware block id to an output tile (tm, tn).  Consecutive
 // hardware ids go to different XCDs; the remap gives each XCD a contiguous
 // run of logical ids, and logical ids walk GROUP_M tile-rows at a time.
