@@ -1057,6 +1057,335 @@ __device__ __forceinline__ void flash_ring_body(const AttnArgs& p) {
   }
 }
 
+// ---- head_dim 128, two wave groups half a step apart ----
+// The two waves sharing a SIMD (w and w + NW/2) run the same work, and with
+// both in the same phase the older one wins every MFMA slot: it finishes its
+// step first and idles at the barrier while the younger one runs alone
+// (s_memtime per wave at the C4 shape: the older waves waited ~1450 cycles
+// per ~4300-cycle step at the barrier, the younger ~180).  Here the two
+// groups order a step's work differently: between two barriers the older
+// group does S^T(e), max(e), P.V(e-1) with exp(e); the younger P.V(e-1),
+// S^T(e), max(e), exp(e).  The younger group's exponentials then run while
+// the older group issues its P.V MFMAs, and its MFMA bursts fall where the
+// older group computes its row max.
+// Lifetimes: K(e) and V(e-1) are read by both groups in epoch e; copies of
+// K(e+2) and V(e+1) go out at the start of epoch e and are waited for at
+// the end of epoch e+1 (three-slot K ring, four-slot V ring).
+// O rescales: O takes the factor of max(e) right after the P.V MFMAs that
+// add tile e-1, the last tile scored at the old reference.
+template <int HD, int NW, bool CAUSAL, bool KMASK>
+__device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
+  constexpr int BM = 32 * NW;
+  constexpr int RB = HD * 2;               // K / V tile row bytes
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  constexpr int TILE = kBN * RB;           // bytes per K or V tile
+  constexpr int COPIES = TILE / 1024;      // 1 KB wave copies per tile
+  constexpr int CPW = COPIES / NW;         // copies per wave per tile
+  constexpr int RPC = 1024 / RB;           // tile rows per copy
+  constexpr int DB = HD / 32;              // 32-row blocks of the O^T accumulator
+  constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
+  constexpr int NS = 2 * KSTEPS;           // S^T MFMAs per tile
+  constexpr int NP = 4 * DB;               // O^T MFMAs per tile
+  constexpr int KSL = 3, VSL = 4;          // ring slots
+  static_assert(HD % 32 == 0 && COPIES % NW == 0 && NW % 2 == 0, "whole copies per wave, two groups");
+
+  __shared__ __attribute__((aligned(16))) char smem[(KSL + VSL) * TILE];
+  const uint32_t lds_base = (uint32_t)(size_t)(lds_char*)smem;
+  auto kslot = [&](int i) { return smem + i * TILE; };
+  auto vslot = [&](int i) { return smem + (KSL + i) * TILE; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = p.B * p.H;
+  const int n_qt = (p.S + BM - 1) / BM;
+  const int id = blockIdx.x;
+  const int qt = CAUSAL ? (n_qt - 1 - id / BH) : id / BH;
+  const int bh = id % BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int q0 = qt * BM;
+
+  const f16* qb = p.q + b * p.qs[0] + h * p.qs[1];
+  const f16* kb = p.k + b * p.ks[0] + h * p.ks[1];
+  const f16* vb = p.v + b * p.vs[0] + h * p.vs[1];
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kvs : nullptr;
+
+  const int my_row = q0 + wave * 32 + (lane & 31);
+  const int g = lane >> 5;
+  const int wave_row_min = q0 + wave * 32;
+
+  f16x8 qf[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if (my_row < p.S)
+      qf[kk] = *reinterpret_cast<const f16x8*>(qb + (int64_t)my_row * p.qs[2] + kk * 16 + g * 8);
+    else
+      qf[kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  wait_copies();  // Q is in registers before any copy is issued
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[d][r] = 0.f;
+  float m_run = -INFINITY;  // running max of scale*log2e*s
+  float l_run = 0.f;        // lane-partial running sum (this lane's keys)
+
+  const int kv_end = CAUSAL ? min(p.S, q0 + BM) : p.S;
+  const int n_kt = (kv_end + kBN - 1) / kBN;
+
+  // ---- copies (the layouts of flash_dma_body) ----
+  int c_row[CPW];
+  const f16* k_src[CPW];
+  const f16* v_src[CPW];
+  int k_col[CPW], v_col[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int ci = wave + i * NW;
+    const int row = ci * RPC + lane / CPR;
+    const int phys = lane % CPR;
+    c_row[i] = row;
+    k_col[i] = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
+    v_col[i] = (phys ^ vswz<RB>(row)) * 8;
+    k_src[i] = kb + (int64_t)row * p.ks[2] + k_col[i];
+    v_src[i] = vb + (int64_t)row * p.vs[2] + v_col[i];
+  }
+  const int64_t k_tile = (int64_t)kBN * p.ks[2], v_tile = (int64_t)kBN * p.vs[2];
+  auto copy_tile = [&](const f16* const (&src)[CPW], const f16* base, int64_t rs, int64_t tstride,
+                       const int (&col)[CPW], int j, uint32_t dst) {
+    if ((j + 1) * kBN <= p.S) {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) dma16(src[i] + j * tstride, dst + (wave + i * NW) * 1024);
+    } else {  // rows past S re-read row S-1 (finite; masked or multiplied by P = 0)
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        const int key = min(j * kBN + c_row[i], p.S - 1);
+        dma16(base + (int64_t)key * rs + col[i], dst + (wave + i * NW) * 1024);
+      }
+    }
+  };
+  // Past the last tile the copies repeat it (same bytes into its own slot, or
+  // a free one), so every epoch issues the same number and the waits stay exact.
+  auto copies = [&](int e) {
+    const int jk = min(e + 2, n_kt - 1), jv = min(e + 1, n_kt - 1);
+    copy_tile(k_src, kb, p.ks[2], k_tile, k_col, jk, lds_base + (jk % KSL) * TILE);
+    copy_tile(v_src, vb, p.vs[2], v_tile, v_col, jv, lds_base + (KSL + jv % VSL) * TILE);
+  };
+
+  // ---- operand reads ----
+  auto read_k = [&](const char* ks_, int c) {  // S^T MFMA c: key block c & 1, k-step c >> 1
+    return *reinterpret_cast<const f16x8*>(ks_ + swz_off<RB>((c & 1) * 32 + (lane & 31), 2 * (c >> 1) + g));
+  };
+  int v_rd[2][DB];
+  {
+    const int tq = lane >> 4, ts = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int row = 8 * r + 4 * (tq >> 1) + (ts >> 2);
+        const int col = 32 * d + 16 * (tq & 1) + 4 * (ts & 3);
+        v_rd[r][d] = row * RB + (((col >> 3) ^ vswz<RB>(row)) << 4) + (col & 7) * 2;
+      }
+  }
+  auto read_v = [&](const char* vs_, int c) -> f16x8 {  // O^T MFMA c: P block c / DB, head-dim block c % DB
+    const int t = c / DB, d = c % DB;
+    const lds_char* base = (const lds_char*)(vs_ + t * 16 * RB);
+    const tr_f16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[0][d]));
+    const tr_f16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr_f16x4*)(base + v_rd[1][d]));
+    return __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi), 0, 1, 2, 3, 4, 5,
+                                   6, 7);
+  };
+  auto key_byte = [&](int kt) { return KMASK ? (int)kvb[min(kt * kBN + lane, p.S - 1)] : 1; };
+  uint64_t kbits_cur = KMASK ? (uint64_t)__ballot(key_byte(0) != 0) : 0ull;  // bit j: key j of the tile valid
+  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
+  constexpr int RA = 3;  // operand reads run this many MFMAs ahead of their use
+
+  // ---- phases ----
+  // S^T(e) into s.  Accumulator entry r of block kb2 is key 64e + 32*kb2 + 8*(r/4) + 4*g + r%4.
+  auto scores = [&](int e, f32x16 (&s)[2]) {
+    const char* ks_ = kslot(e % KSL);
+    f16x8 kfr[NS];
+#pragma unroll
+    for (int c = 0; c < RA; ++c) kfr[c] = read_k(ks_, c);
+#pragma unroll
+    for (int c = 0; c < NS; ++c) {
+      if (c + RA < NS) kfr[c + RA] = read_k(ks_, c + RA);
+      const int kb2 = c & 1, kk = c >> 1;
+      s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfr[c], qf[kk], kk == 0 ? f32x16{} : s[kb2], 0, 0, 0);
+    }
+  };
+  // Mask and row max of S(e); moves the reference (lazy rescale, as
+  // flash_dma_body) and scales l.  Returns the O factor and whether to apply it.
+  auto row_max = [&](int e, f32x16 (&s)[2], float& alpha) -> bool {
+    const int k0 = e * kBN;
+    float mx = -INFINITY;
+    const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
+    if (need_mask) {
+      const uint64_t kbits = kbits_cur >> (4 * g);  // bit j: key k0 + 4*g + j is valid
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = kb2 * 32 + 8 * (r >> 2) + (r & 3);
+          const int key = k0 + j + 4 * g;
+          if (key >= p.S || (CAUSAL && key > my_row) || (KMASK && ((kbits >> j) & 1) == 0))
+            s[kb2][r] = -INFINITY;
+          mx = fmaxf(mx, s[kb2][r]);
+        }
+    } else {
+#pragma unroll
+      for (int e2 = 0; e2 < 32; ++e2) mx = fmaxf(mx, s[e2 >> 4][e2 & 15]);
+    }
+    mx = pair_max(mx);
+    const float m_tile = mx * p.scale_log2;  // scale > 0: max(s)*c == max(s*c)
+    const bool rescale = __any(m_tile > m_run + 8.0f);
+    alpha = 1.0f;
+    if (rescale) {
+      const float m_new = fmaxf(m_run, m_tile);
+      alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+    }
+    return rescale;
+  };
+  // O^T += V^T(j) . P^T(j) (pv_on) interleaved with the exponentials of s into pn.
+  auto pv_exp = [&](bool pv_on, int j, const f16x8 (&pp)[4], const f32x16 (&s)[2], f16x8 (&pn)[4]) {
+    const float cs = p.scale_log2;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    const char* vs_ = vslot(((j % VSL) + VSL) % VSL);
+    f16x8 vfr[NP];
+    if (pv_on) {
+#pragma unroll
+      for (int c = 0; c < RA; ++c) vfr[c] = read_v(vs_, c);
+    }
+    float ls = 0.f;
+    constexpr int EPM = 32 / NP;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      if (pv_on) {
+        if (c + RA < NP) vfr[c + RA] = read_v(vs_, c + RA);
+        acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vfr[c], pp[c / DB], acc_o[c % DB], 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = c * EPM; e < (c + 1) * EPM; e += 2) {
+        const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use)),
+                          (f16)__builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use))};
+        pn[e >> 3][e & 7] = hp[0];
+        pn[e >> 3][(e & 7) + 1] = hp[1];
+        ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+      }
+    }
+    l_run += ls;
+  };
+  auto pv_only = [&](int j, const f16x8 (&pp)[4]) {
+    const char* vs_ = vslot(j % VSL);
+#pragma unroll
+    for (int c = 0; c < NP; ++c)
+      acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(vs_, c), pp[c / DB], acc_o[c % DB], 0, 0, 0);
+  };
+  auto scale_o = [&](float alpha) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
+  };
+  // End of epoch e: this epoch's copies may stay in flight, the previous
+  // epoch's have landed; the next tile's key bits; barrier.
+  auto epoch_end = [&](int e, int kbyte_next) {
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * CPW>();
+    if (KMASK && e + 1 < n_kt) kbits_cur = (uint64_t)__ballot(kbyte_next != 0);
+    lds_barrier();
+  };
+  auto next_key_byte = [&](int e) { return (KMASK && e + 1 < n_kt) ? key_byte(e + 1) : 1; };
+
+  // ---- prologue: K(0), K(1), V(0) resident ----
+  copy_tile(k_src, kb, p.ks[2], k_tile, k_col, 0, lds_base);
+  {
+    const int j1 = min(1, n_kt - 1);
+    copy_tile(k_src, kb, p.ks[2], k_tile, k_col, j1, lds_base + (j1 % KSL) * TILE);
+  }
+  copy_tile(v_src, vb, p.vs[2], v_tile, v_col, 0, lds_base + KSL * TILE);
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  f32x16 s[2];
+  f16x8 pf_a[4], pf_b[4];
+  const bool older = wave < NW / 2;
+  if (older) {
+    // epoch e: copies; S(e); max(e); P.V(e-1) with exp(e); O rescale; barrier
+    auto epoch = [&](int e, f16x8 (&pc)[4], const f16x8 (&pp)[4]) {
+      const int kbn = next_key_byte(e);
+      copies(e);
+      scores(e, s);
+      float alpha;
+      const bool rs = row_max(e, s, alpha);
+      pv_exp(e > 0, e - 1, pp, s, pc);
+      if (rs) scale_o(alpha);
+      epoch_end(e, kbn);
+    };
+    int e = 0;
+    for (; e + 1 < n_kt; e += 2) {
+      epoch(e, pf_a, pf_b);
+      epoch(e + 1, pf_b, pf_a);
+    }
+    wait_vmcnt<0>();
+    if (e < n_kt) {
+      epoch(e, pf_a, pf_b);
+      wait_vmcnt<0>();
+      pv_only(n_kt - 1, pf_a);
+    } else {
+      pv_only(n_kt - 1, pf_b);
+    }
+  } else {
+    // epoch e: copies; P.V(e-1); S(e); max(e); exp(e); O rescale (O holds
+    // the tiles < e, added at the old reference); barrier.  P crosses the
+    // barrier, the scores do not.
+    auto epoch = [&](int e, f16x8 (&pc)[4], const f16x8 (&pp)[4]) {
+      const int kbn = next_key_byte(e);
+      copies(e);
+      if (e > 0) pv_only(e - 1, pp);
+      scores(e, s);
+      float alpha;
+      const bool rs = row_max(e, s, alpha);
+      pv_exp(false, 0, pp, s, pc);
+      if (rs) scale_o(alpha);
+      epoch_end(e, kbn);
+    };
+    int e = 0;
+    for (; e + 1 < n_kt; e += 2) {
+      epoch(e, pf_a, pf_b);
+      epoch(e + 1, pf_b, pf_a);
+    }
+    wait_vmcnt<0>();
+    if (e < n_kt) {
+      epoch(e, pf_a, pf_b);
+      wait_vmcnt<0>();
+      pv_only(n_kt - 1, pf_a);
+    } else {
+      pv_only(n_kt - 1, pf_b);
+    }
+  }
+
+  // ---- normalise and store: lane holds O[row][d], d = 32*db + 8*(r/4) + 4*g + r%4 ----
+  l_run = pair_sum(l_run);
+  const float inv = 1.0f / l_run;
+  if (my_row < p.S) {
+    f16* ob = p.o + b * p.os[0] + h * p.os[1] + (int64_t)my_row * p.os[2];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int dd = d * 32 + 8 * q + 4 * g;
+        f16x4 t = {(f16)(acc_o[d][4 * q] * inv), (f16)(acc_o[d][4 * q + 1] * inv),
+                   (f16)(acc_o[d][4 * q + 2] * inv), (f16)(acc_o[d][4 * q + 3] * inv)};
+        *reinterpret_cast<f16x4*>(ob + dd) = t;
+      }
+  }
+}
+
 // ---- one key tile (S <= 64, head_dim <= 64) ----
 // Short sequences are latency-bound (the reference's B256 S64 config runs
 // 2048 heads of one tile each): a workgroup loads Q, one K and one V tile
@@ -1316,7 +1645,9 @@ __global__ __launch_bounds__(NW * 64, (NW <= 4 && HD <= 64) ? 2 : 1) void flash_
   // 1263-1295 -> 1180-1199 us in alternating same-box runs); without the
   // causal diagonal the register body stays (its ring build spills ~100 B
   // there: b2 s4096 non-causal 318-340 vs 354 us).
-  if constexpr (HD == 128 && CAUSAL) {
+  if constexpr (HD == 128 && CAUSAL && NW == 8) {
+    flash_pair_body<HD, NW, CAUSAL, KMASK>(p);  // C4 b4 s8192: 1268-1300 -> 1225-1263 us against the ring body
+  } else if constexpr (HD == 128 && CAUSAL) {
     flash_ring_body<HD, NW, CAUSAL, KMASK>(p);
   } else if constexpr (HD == 128) {
     flash_vreg_body<HD, NW, CAUSAL, KMASK>(p);
