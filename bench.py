@@ -152,9 +152,11 @@ def parse_shape(text: str) -> tuple:
 CPU_FLOP_CAP = 4e12
 
 
-def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str):
-    """Time the fp32 CPU oracle on a bounded sample of the workload; when the
-    sample is the whole forward, also check the GPU output against it.
+def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str, mask_host=None):
+    """Time the fp32 CPU oracle on a bounded sample of the workload and check
+    the GPU output rows the sample covers.  A padded input (``mask_host`` not
+    all-true) is sampled only where the whole forward fits the CPU leg (the
+    query-chunked oracle is dense-only).
     Returns (cpu_baseline dict or None, parity dict or None)."""
     from oracle import baseline as ob  # the CPU baseline and its parity check only
 
@@ -172,11 +174,11 @@ def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str):
     xs_full = x_host.float()
     parity = None
     if full:
-        fn = None
+        fn = None if mask_host is None else (lambda t: base(t, mask_host))  # noqa: E731
         xs, sample_b = xs_full, b
         sample = f"full {label} forward (B{b} S{s}), median of 3 after 1 warmup"
         reps, warm = 3, 1
-    elif flop_per_sample <= CPU_FLOP_CAP:
+    elif flop_per_sample <= CPU_FLOP_CAP and (mask_host is None or bool(mask_host.all())):
         xs, sample_b = xs_full[:1], 1
         fn = lambda t: ob.chunked_forward(base, t, q_chunk=2048)  # noqa: E731
         sample = (f"query-chunked fp32 oracle (row-exact to the baseline), sequence 0 of the batch of {b}, "
@@ -186,6 +188,8 @@ def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str):
         return None, None
     outs = []
     keep = (lambda t: outs.append(fn(t))) if fn is not None else None
+    if full and fn is not None:  # padded: the full forward with its mask
+        keep = fn
     ts = ob.time_cpu_forward(base, xs, warmup=warm, repeats=reps, fn=keep)
     cpu_fwd = statistics.median(ts) * (b / sample_b)
     cpu = {
@@ -199,7 +203,7 @@ def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str):
     if out_gpu is not None:
         if full:
             with torch.inference_mode():
-                ref = base(xs)
+                ref = base(xs) if mask_host is None else base(xs, mask_host)
             got, rows = out_gpu, "every row"
         else:  # the sampled sequence's output from the timed chunked call
             ref, got, rows = outs[-1], out_gpu[:sample_b], f"sequence 0 of {b} (all {s} rows)"
@@ -231,6 +235,9 @@ def main() -> int:
     ap.add_argument("--dispatch", nargs="?", const="default", default=None,
                     help="apply the per-shape settings table (tkmi/configs/dispatch.json, or the path given); "
                          "--graph / --unfused-norm given here win")
+    ap.add_argument("--padding-ratio", type=float, default=0.0,
+                    help="prefix padding masks as the harness's --padding-ratio draws them "
+                         "(src/torch_transformer_benchmark.py:255-271); 0 = dense")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -288,7 +295,14 @@ def main() -> int:
     gen = torch.Generator().manual_seed(1234 + 100000)
     x = torch.randn(b, s, d, generator=gen).to(dtype)
     mask = torch.ones(b, s, dtype=torch.bool)
-    x_host = x
+    if args.padding_ratio > 0:
+        # the harness's recipe: per-sequence prefix lengths drawn from the same
+        # generator after x, padded positions of x zeroed
+        min_valid = max(1, int(round(s * (1.0 - args.padding_ratio))))
+        lengths = torch.randint(low=min_valid, high=s + 1, size=(b,), generator=gen)
+        mask = torch.arange(s)[None, :] < lengths[:, None]
+        x = x.masked_fill(~mask[..., None], 0)
+    x_host, mask_host = x, mask
     x, mask = x.to(dev), mask.to(dev)
 
     with torch.inference_mode():
@@ -358,7 +372,7 @@ def main() -> int:
     cpu, parity = None, None
     if not args.no_cpu_baseline:
         cpu, parity = cpu_baseline_leg(model, cfg_t, x_host, out_gpu=None if args.no_check else got_gpu,
-                                       label=workload)
+                                       label=workload, mask_host=mask_host if args.padding_ratio > 0 else None)
 
     t = b * s
     line = {
@@ -379,7 +393,7 @@ def main() -> int:
             "workload": f"{workload}: B{b} S{s} D{d} H{h} F{f} L{nl} {'causal' if causal else 'non-causal'}",
             "batch": b, "seq_len": s, "d_model": d, "heads": h, "ffn_dim": f, "layers": nl,
             "causal": causal, "parallelism": "single GPU", "fused_norm": not args.unfused_norm,
-            "hip_graph": bool(args.graph), "dispatch": chosen,
+            "hip_graph": bool(args.graph), "dispatch": chosen, "padding_ratio": args.padding_ratio,
         },
         "tokens_per_s": round(t * 1000.0 / fwd_ms, 1),
         "wall_s_timed": round(wall, 4),
