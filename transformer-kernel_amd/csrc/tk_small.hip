@@ -3,23 +3,28 @@
 // appendix shapes, where the layer-by-layer path is ~36 launches of a few
 // microseconds each per forward.
 //
-// One workgroup (4 waves) runs the complete forward of one sequence, all
-// layers, without touching HBM between kernels:
+// One workgroup runs the complete forward of one sequence, all layers,
+// without touching HBM between kernels.  8 waves (two per SIMD, so one
+// wave's LDS, L2 and barrier latency overlaps the other's MFMAs; 4 waves
+// when S <= 32 leaves a single row block):
 //   * the fp32 residual stream x stays in registers for the whole forward:
-//     wave w owns columns [32w, 32w+32) of every row, in the 32x32 MFMA
-//     accumulator layout of C^T (lane l holds 4 consecutive columns of row
-//     32*mb + (l & 31) per 4 registers), so the out-projection and FFN-down
-//     products accumulate straight into it;
-//   * LayerNorm row statistics are combined across the 4 waves through a
-//     small LDS table (exact two-pass mean / variance);
+//     wave w owns columns [32c, 32c+32), c = w & 3, of the row blocks
+//     (w >> 2) and (w >> 2) + 2, in the 32x32 MFMA accumulator layout of C^T
+//     (lane l holds 4 consecutive columns of row 32*mb + (l & 31) per 4
+//     registers), so the out-projection and FFN-down products accumulate
+//     straight into it;
+//   * LayerNorm row statistics are combined across the 4 column waves of a
+//     row through a small LDS table (exact two-pass mean / variance);
 //   * the GEMMs compute C^T = W . A^T on v_mfma_f32_32x32x16_f16: the A
 //     operand is a weight fragment (16 bytes per lane, read from L2 one phase
-//     ahead of its use), the B operand an activation fragment from a
-//     chunk-swizzled LDS tile (h, Q, K, ctx, u);
-//   * attention: S^T = K . Q^T per 32-row query block over at most 4 key
-//     blocks, fp32 scores, -inf masking, exact row max, exp2 with the scale
-//     folded, fp16 P, row sums of the fp16 P, O^T = V^T . P^T with V^T from
-//     ds_read_b64_tr_b16 reads of the row-major V tile.
+//     ahead of its use, the QKV blocks one block ahead), the B operand an
+//     activation fragment from a chunk-swizzled LDS tile (h, Q, K, ctx, u);
+//   * attention: one item per (head, 32-row query block), items dealt to
+//     the waves heaviest first; S^T = K . Q^T per 32-key block with FA-2
+//     online softmax across the at most 4 key blocks (fp32 scores, -inf
+//     masking, running max, exp2 with the scale folded, fp16 P, row sums of
+//     the fp16 P, O rescaled when the max grows), O^T = V^T . P^T with V^T
+//     from ds_read_b64_tr_b16 reads of the row-major V tile.
 // Numerics are those of the layer-by-layer path (src/optimized.py:488-554;
 // src/kernels.py:112-134): fp16 operands, fp32 accumulation, residual and
 // statistics, bias/GELU/residual in fp32 before each fp16 rounding.
@@ -73,11 +78,11 @@ __device__ __forceinline__ void lds_sync() {
 }
 
 template <int D, int DP, int F, int HDP, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
-  static_assert(D == 128 && DP == 128 && F == 128, "one width: 4 waves x 32 columns");
+__global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
+  static_assert(D == 128 && DP == 128 && F == 128, "one width: 4 column waves x 32 columns");
   static_assert(HDP == 16 || HDP == 32 || HDP == 64 || HDP == 128, "head dims with an MFMA k-step");
   constexpr int KD = D / 16, KP = DP / 16, KF = F / 16;  // k-steps
-  constexpr int NQ = 3 * DP / 32 / 4;                      // QKV n-blocks per wave
+  constexpr int NQ = 3 * DP / 32 / 4;                      // QKV n-blocks per column wave
   constexpr int HK = HDP / 16;                             // k-steps of one head
   constexpr int DB = (HDP + 31) / 32;                      // 32-row blocks of O^T
 
@@ -85,44 +90,52 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
   // b_qkv | b_o | b_1 | b_2 | n1_w | n1_b | n2_w | n2_b, then the final norm.
   constexpr int V_BO = 3 * DP, V_B1 = V_BO + D, V_B2 = V_B1 + F, V_N1W = V_B2 + D, V_N1B = V_N1W + D,
                 V_N2W = V_N1B + D, V_N2B = V_N2W + D, VEC = V_N2B + D;
-  constexpr int VPT = VEC / 256;  // vector floats per thread
-  static_assert(VEC % 256 == 0, "whole vector rows per thread");
+  static_assert(3 * DP <= 512, "b_qkv: at most two elements per thread of 256");
 
   __shared__ __attribute__((aligned(16))) char smem[4 * kTile + 2 * 4 * kMaxRows * 4 + (2 * VEC + 2 * D) * 4];
   char* Ht = smem;                // h (LayerNorm output) / ctx
   char* Qt = smem + kTile;        // Q / u
   char* Kt = smem + 2 * kTile;    // K
   char* Vt = smem + 3 * kTile;    // V
-  float* stats = reinterpret_cast<float*>(smem + 4 * kTile);  // [2][4 waves][128 rows]
+  float* stats = reinterpret_cast<float*>(smem + 4 * kTile);  // [2][4 column waves][128 rows]
   float* vecs = stats + 2 * 4 * kMaxRows;                     // [2][VEC], then nf_w, nf_b
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane >> 5;
-  const int rl = lane & 31;
+  const int wc = w & 3;   // column block: columns [32 wc, 32 wc + 32) of every 128-wide product
+  const int rh = w >> 2;  // row blocks rh and rh + 2
+  // Lane coordinates.  refresh() passes them through an empty asm at the
+  // start of each phase, so the LDS addresses derived from them (one per
+  // swizzled 16-byte chunk) are recomputed per phase instead of being hoisted
+  // out of the layer loop and held in registers for the whole forward.
+  int g = lane >> 5;
+  int rl = lane & 31;
+  int tq = lane >> 4, ts = lane & 15;
+  auto refresh = [&]() { asm volatile("" : "+v"(g), "+v"(rl), "+v"(tq), "+v"(ts)); };
   const int S = p.S;
   const int MB = (S + 31) >> 5;
   const int64_t b = blockIdx.x;
   const float* xb = p.x + b * (int64_t)S * D;
   float* ob = p.out + b * (int64_t)S * D;
 
-  // ---- residual stream: columns 32w + 8q + 4g + e of row 32mb + rl ----
-  f32x16 xr[4];
+  // ---- residual stream: columns 32wc + 8q + 4g + e of row 32(rh + 2i) + rl ----
+  f32x16 xr[2];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const int m = mb * 32 + rl;
+  for (int i = 0; i < 2; ++i) {
+    const int m = (rh + 2 * i) * 32 + rl;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (m < S) v = *reinterpret_cast<const f32x4*>(xb + (int64_t)m * D + 32 * w + 8 * q + 4 * g);
+      if (m < S) v = *reinterpret_cast<const f32x4*>(xb + (int64_t)m * D + 32 * wc + 8 * q + 4 * g);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = v[e];
+      for (int e = 0; e < 4; ++e) xr[i][4 * q + e] = v[e];
     }
   }
 
   // ---- weight fragments (A operand): W[n0 + rl][16*kk + 8g .. +8] ----
+  // (wave-uniform base + 32-bit lane offset: the scalar-base addressing form)
   auto wfrag = [&](const f16* W, int K, int n0, int kk) {
-    return *reinterpret_cast<const f16x8*>(W + (int64_t)(n0 + rl) * K + kk * 16 + 8 * g);
+    return *reinterpret_cast<const f16x8*>(W + (uint32_t)((n0 + rl) * K + 8 * g) + kk * 16);
   };
   // activation fragment (B operand): tile row r, k-step kk (+ chunk offset c0)
   auto afrag = [&](const char* T, int r, int c0, int kk) {
@@ -133,52 +146,53 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
     *reinterpret_cast<f16x4*>(T + act_off(r, n >> 3) + (n & 7) * 2) = t;
   };
 
-  // ---- LayerNorm of the residual stream (exact two passes over 4 waves) ----
+  // ---- LayerNorm of the residual stream (exact two passes over the 4 column waves) ----
   // FINAL: fp32 to the output; else fp16 into the h tile.
   auto layer_norm = [&](const float* gw, const float* gb, float eps, auto final_c) {
     constexpr bool FINAL = decltype(final_c)::value;
-    float mean[4], rstd[4];
+    refresh();
+    float mean[2], rstd[2];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int i = 0; i < 2; ++i) {
       float s = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += xr[mb][r];
+      for (int r = 0; r < 16; ++r) s += xr[i][r];
       s = pair_sum(s);
-      if (g == 0) stats[w * kMaxRows + mb * 32 + rl] = s;
+      if (g == 0) stats[wc * kMaxRows + (rh + 2 * i) * 32 + rl] = s;
     }
     lds_sync();
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = mb * 32 + rl;
-      mean[mb] = (stats[m] + stats[kMaxRows + m] + stats[2 * kMaxRows + m] + stats[3 * kMaxRows + m]) / (float)D;
+    for (int i = 0; i < 2; ++i) {
+      const int m = (rh + 2 * i) * 32 + rl;
+      mean[i] = (stats[m] + stats[kMaxRows + m] + stats[2 * kMaxRows + m] + stats[3 * kMaxRows + m]) / (float)D;
       float s = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float d = xr[mb][r] - mean[mb];
+        const float d = xr[i][r] - mean[i];
         s += d * d;
       }
       s = pair_sum(s);
-      if (g == 0) stats[4 * kMaxRows + w * kMaxRows + m] = s;
+      if (g == 0) stats[4 * kMaxRows + wc * kMaxRows + m] = s;
     }
     lds_sync();
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = mb * 32 + rl;
+    for (int i = 0; i < 2; ++i) {
+      const int m = (rh + 2 * i) * 32 + rl;
       const float* s2 = stats + 4 * kMaxRows;
       const float var = (s2[m] + s2[kMaxRows + m] + s2[2 * kMaxRows + m] + s2[3 * kMaxRows + m]) / (float)D;
-      rstd[mb] = 1.0f / sqrtf(var + eps);
+      rstd[i] = 1.0f / sqrtf(var + eps);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = 32 * w + 8 * q + 4 * g;
+      const int n = 32 * wc + 8 * q + 4 * g;
       const f32x4 wv = *reinterpret_cast<const f32x4*>(gw + n);
       const f32x4 bv = *reinterpret_cast<const f32x4*>(gb + n);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int m = mb * 32 + rl;
+      for (int i = 0; i < 2; ++i) {
+        const int m = (rh + 2 * i) * 32 + rl;
         float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (xr[mb][4 * q + e] - mean[mb]) * rstd[mb] * wv[e] + bv[e];
+        for (int e = 0; e < 4; ++e) y[e] = (xr[i][4 * q + e] - mean[i]) * rstd[i] * wv[e] + bv[e];
         if constexpr (FINAL) {
           if (m < S) *reinterpret_cast<f32x4*>(ob + (int64_t)m * D + n) = f32x4{y[0], y[1], y[2], y[3]};
         } else {
@@ -188,52 +202,63 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
     }
   };
 
-  f16x8 wq[NQ][KD], wo[KP], w1[KD], w2[KF];
-  auto load_wq = [&](int l) {
+  // QKV weight blocks go through a two-deep buffer (block j in wq[j & 1]),
+  // the others one phase ahead: at most two phases' fragments are live.
+  f16x8 wq[2][KD], wo[KP], w1[KD], w2[KF];
+  auto load_wq = [&](int l, int j) {
     const f16* W = p.w_qkv + (int64_t)l * 3 * DP * D;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j)
-#pragma unroll
-      for (int kk = 0; kk < KD; ++kk) wq[j][kk] = wfrag(W, D, 32 * (w + 4 * j), kk);
+    for (int kk = 0; kk < KD; ++kk) wq[j & 1][kk] = wfrag(W, D, 32 * (wc + 4 * j), kk);
   };
   auto load_wo = [&](int l) {
 #pragma unroll
-    for (int kk = 0; kk < KP; ++kk) wo[kk] = wfrag(p.w_o + (int64_t)l * D * DP, DP, 32 * w, kk);
+    for (int kk = 0; kk < KP; ++kk) wo[kk] = wfrag(p.w_o + (int64_t)l * D * DP, DP, 32 * wc, kk);
   };
   auto load_w1 = [&](int l) {
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk) w1[kk] = wfrag(p.w_1 + (int64_t)l * F * D, D, 32 * w, kk);
+    for (int kk = 0; kk < KD; ++kk) w1[kk] = wfrag(p.w_1 + (int64_t)l * F * D, D, 32 * wc, kk);
   };
   auto load_w2 = [&](int l) {
 #pragma unroll
-    for (int kk = 0; kk < KF; ++kk) w2[kk] = wfrag(p.w_2 + (int64_t)l * D * F, F, 32 * w, kk);
+    for (int kk = 0; kk < KF; ++kk) w2[kk] = wfrag(p.w_2 + (int64_t)l * D * F, F, 32 * wc, kk);
   };
 
   // V^T fragment offsets (see flash_dma_body): lane = 16*tq + ts covers
   // keys 16t + 8r + 4*(tq >> 1) + (ts >> 2), columns 32db + 16*(tq & 1) + 4*(ts & 3).
-  const int tq = lane >> 4, ts = lane & 15;
-  const bool d_ok = HDP % 32 == 0 || rl < HDP;
+  const bool d_ok = HDP % 32 == 0 || (lane & 31) < HDP;
   const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
 
-  // layer l's vectors: thread t holds elements t + 256*i
-  auto vec_src = [&](int l, int idx) -> float {
-    if (idx < V_BO) return p.b_qkv[(int64_t)l * 3 * DP + idx];
-    if (idx < V_B1) return p.b_o[(int64_t)l * D + idx - V_BO];
-    if (idx < V_B2) return p.b_1[(int64_t)l * F + idx - V_B1];
-    if (idx < V_N1W) return p.b_2[(int64_t)l * D + idx - V_B2];
-    if (idx < V_N1B) return p.n1_w[(int64_t)l * D + idx - V_N1W];
-    if (idx < V_N2W) return p.n1_b[(int64_t)l * D + idx - V_N1B];
-    if (idx < V_N2B) return p.n2_w[(int64_t)l * D + idx - V_N2W];
-    return p.n2_b[(int64_t)l * D + idx - V_N2B];
-  };
-  float vreg[VPT];
+  // layer l's vectors: thread t holds element t of each (b_qkv: elements t
+  // and t + 256 with 256 threads), read from the arrays' layer-l rows.
+  const int tid = threadIdx.x;
+  const bool two_qkv = blockDim.x == 256;
+  float vreg[9];
   auto vec_load = [&](int l) {
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) vreg[i] = vec_src(l, threadIdx.x + 256 * i);
+    if (tid < 3 * DP) vreg[0] = (p.b_qkv + l * 3 * DP)[(uint32_t)tid];
+    if (two_qkv && tid + 256 < 3 * DP) vreg[8] = (p.b_qkv + l * 3 * DP)[(uint32_t)(tid + 256)];
+    if (tid < D) {
+      vreg[1] = (p.b_o + l * D)[(uint32_t)tid];
+      vreg[2] = (p.b_1 + l * F)[(uint32_t)tid];
+      vreg[3] = (p.b_2 + l * D)[(uint32_t)tid];
+      vreg[4] = (p.n1_w + l * D)[(uint32_t)tid];
+      vreg[5] = (p.n1_b + l * D)[(uint32_t)tid];
+      vreg[6] = (p.n2_w + l * D)[(uint32_t)tid];
+      vreg[7] = (p.n2_b + l * D)[(uint32_t)tid];
+    }
   };
   auto vec_store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) vecs[buf * VEC + threadIdx.x + 256 * i] = vreg[i];
+    float* v = vecs + buf * VEC;
+    if (tid < 3 * DP) v[tid] = vreg[0];
+    if (two_qkv && tid + 256 < 3 * DP) v[tid + 256] = vreg[8];
+    if (tid < D) {
+      v[V_BO + tid] = vreg[1];
+      v[V_B1 + tid] = vreg[2];
+      v[V_B2 + tid] = vreg[3];
+      v[V_N1W + tid] = vreg[4];
+      v[V_N1B + tid] = vreg[5];
+      v[V_N2W + tid] = vreg[6];
+      v[V_N2B + tid] = vreg[7];
+    }
   };
   vec_load(0);
   vec_store(0);
@@ -241,26 +266,31 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
     vecs[2 * VEC + threadIdx.x] = p.nf_w[threadIdx.x];
     vecs[2 * VEC + D + threadIdx.x] = p.nf_b[threadIdx.x];
   }
-  load_wq(0);
+  load_wq(0, 0);
   lds_sync();  // vectors of layer 0 and the final norm staged
   layer_norm(vecs + V_N1W, vecs + V_N1B, p.n1_eps, std::false_type{});
+  // Attention work items: (head, 32-row query block), heaviest first (causal
+  // cost grows with the block index), dealt to the NWV waves in snake order.
+  const int items = p.H * MB;
+  const int NWV = blockDim.x >> 6;
   for (int l = 0; l < p.L; ++l) {
     lds_sync();  // h complete
     // ---- QKV = h . W_qkv^T + b -> Q, K, V tiles ----
     {
+      refresh();
       const float* bq = vecs + (l & 1) * VEC;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb >= MB) break;
-        f16x8 hf[KD];
+      for (int j = 0; j < NQ; ++j) {
+        if (j + 1 < NQ) load_wq(l, j + 1);
 #pragma unroll
-        for (int kk = 0; kk < KD; ++kk) hf[kk] = afrag(Ht, mb * 32 + rl, 0, kk);
-#pragma unroll
-        for (int j = 0; j < NQ; ++j) {
+        for (int i = 0; i < 2; ++i) {
+          const int mb = rh + 2 * i;
+          if (mb >= MB) break;
           f32x16 acc = {};
 #pragma unroll
-          for (int kk = 0; kk < KD; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[j][kk], hf[kk], acc, 0, 0, 0);
-          const int nb = w + 4 * j;  // 32-column block of [Q | K | V]
+          for (int kk = 0; kk < KD; ++kk)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[j & 1][kk], afrag(Ht, mb * 32 + rl, 0, kk), acc, 0, 0, 0);
+          const int nb = wc + 4 * j;  // 32-column block of [Q | K | V]
           const int part = nb / (DP / 32), col0 = (nb % (DP / 32)) * 32;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -283,61 +313,64 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
     load_wo(l);
     if (l + 1 < p.L) vec_load(l + 1);
     lds_sync();  // Q, K, V complete
-    // ---- attention: heads w, w+4, ...; ctx -> h tile ----
-    for (int hh = w; hh < p.H; hh += 4) {
+    // ---- attention over this wave's (head, query block) items; ctx -> h tile ----
+    for (int k = 0; k < items; ++k) {
+      refresh();
+      const int kr = k % (2 * NWV);
+      if ((kr < NWV ? kr : 2 * NWV - 1 - kr) != w) continue;
+      const int qb = MB - 1 - k / p.H;
+      const int hh = k % p.H;
       const int hc = hh * HDP / 8;  // first chunk of this head's columns
+      const int row = qb * 32 + rl;
+      f16x8 qf[HK];
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
-        if (qb >= MB) break;
-        const int row = qb * 32 + rl;
-        f16x8 qf[HK];
+      for (int kk = 0; kk < HK; ++kk) qf[kk] = afrag(Qt, row, hc, kk);
+      const int kb_end = CAUSAL ? qb + 1 : MB;
+      // Online softmax over the 32-key blocks (S^T = K . Q^T: a lane holds 16
+      // keys of query `row`, its partner lane the other 16): running max m_run
+      // (in exp2 units), O and the row sum rescaled when it grows.  Key block
+      // 0 holds a valid key for every row, so m_run is finite from there on.
+      const float cs = p.scale_log2;
+      float m_run = -INFINITY, ls = 0.f;
+      f32x16 oacc[DB];
 #pragma unroll
-        for (int kk = 0; kk < HK; ++kk) qf[kk] = afrag(Qt, row, hc, kk);
-        const int kb_end = CAUSAL ? qb + 1 : MB;
-        f32x16 sacc[4];
-        float mx = -INFINITY;
+      for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          if (kb < kb_end) {
-            f32x16 a = {};
+      for (int kb = 0; kb < 4; ++kb) {
+        if (kb < kb_end) {
+          f32x16 a = {};
 #pragma unroll
-            for (int kk = 0; kk < HK; ++kk)
-              a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk), qf[kk], a, 0, 0, 0);
+          for (int kk = 0; kk < HK; ++kk)
+            a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk), qf[kk], a, 0, 0, 0);
+          float mx = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-              if (key >= S || (CAUSAL && key > row)) a[r] = -INFINITY;
-              mx = fmaxf(mx, a[r]);
-            }
-            sacc[kb] = a;
+          for (int r = 0; r < 16; ++r) {
+            const int key = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (key >= S || (CAUSAL && key > row)) a[r] = -INFINITY;
+            mx = fmaxf(mx, a[r]);
           }
-        }
-        mx = pair_max(mx);
-        const float cs = p.scale_log2;
-        const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
-        const float m_use = m_tile == -INFINITY ? 0.f : m_tile;
-        f16x8 pf[8];
-        float ls = 0.f;
+          const float m_new = fmaxf(m_run, pair_max(mx) * cs);  // cs > 0: max(s)*cs == max(s*cs)
+          if (kb > 0) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            ls *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          if (kb < kb_end) {
+            for (int d = 0; d < DB; ++d)
 #pragma unroll
-            for (int e = 0; e < 16; e += 2) {
-              const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(sacc[kb][e], cs, -m_use)),
-                                (f16)__builtin_amdgcn_exp2f(fmaf(sacc[kb][e + 1], cs, -m_use))};
-              pf[2 * kb + (e >> 3)][e & 7] = hp[0];
-              pf[2 * kb + (e >> 3)][(e & 7) + 1] = hp[1];
-              ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
-            }
+              for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
           }
-        }
-        const float inv = 1.0f / pair_sum(ls);
-        f32x16 oacc[DB];
+          m_run = m_new;
+          f16x8 pf[2];
 #pragma unroll
-        for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+          for (int e = 0; e < 16; e += 2) {
+            const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(a[e], cs, -m_new)),
+                              (f16)__builtin_amdgcn_exp2f(fmaf(a[e + 1], cs, -m_new))};
+            pf[e >> 3][e & 7] = hp[0];
+            pf[e >> 3][(e & 7) + 1] = hp[1];
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+          }
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          if (t < 2 * kb_end) {
+          for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * kb + tt;
 #pragma unroll
             for (int d = 0; d < DB; ++d) {
               f16x4 half[2];
@@ -351,31 +384,34 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
               }
               f16x8 vf = __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7);
               if (!d_ok) vf = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-              oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], oacc[d], 0, 0, 0);
+              oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[tt], oacc[d], 0, 0, 0);
             }
           }
         }
-        // lane holds O[row][32d + 8q + 4g + e]
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int dd = 32 * d + 8 * q + 4 * g;
-            if (dd < HDP) {
-              const float v[4] = {oacc[d][4 * q] * inv, oacc[d][4 * q + 1] * inv, oacc[d][4 * q + 2] * inv,
-                                  oacc[d][4 * q + 3] * inv};
-              store_h4(Ht, row, hh * HDP + dd, v);
-            }
-          }
       }
+      const float inv = 1.0f / pair_sum(ls);
+      // lane holds O[row][32d + 8q + 4g + e]
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int dd = 32 * d + 8 * q + 4 * g;
+          if (dd < HDP) {
+            const float v[4] = {oacc[d][4 * q] * inv, oacc[d][4 * q + 1] * inv, oacc[d][4 * q + 2] * inv,
+                                oacc[d][4 * q + 3] * inv};
+            store_h4(Ht, row, hh * HDP + dd, v);
+          }
+        }
     }
     load_w1(l);
     lds_sync();  // ctx complete
     // ---- x += ctx . W_o^T + b_o ----
     {
-      const f32x4* bo4 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_BO + 32 * w + 4 * g);
+      refresh();
+      const f32x4* bo4 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_BO + 32 * wc + 4 * g);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+      for (int i = 0; i < 2; ++i) {
+        const int mb = rh + 2 * i;
         if (mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
@@ -385,7 +421,7 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
         for (int q = 0; q < 4; ++q) {
           const f32x4 bv = bo4[2 * q];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = xr[mb][4 * q + e] + (acc[4 * q + e] + bv[e]);
+          for (int e = 0; e < 4; ++e) xr[i][4 * q + e] = xr[i][4 * q + e] + (acc[4 * q + e] + bv[e]);
         }
       }
     }
@@ -394,9 +430,11 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
     lds_sync();  // h complete
     // ---- u = gelu(h . W_1^T + b_1) -> u tile (reuses Q) ----
     {
-      const f32x4* b14 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B1 + 32 * w + 4 * g);
+      refresh();
+      const f32x4* b14 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B1 + 32 * wc + 4 * g);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+      for (int i = 0; i < 2; ++i) {
+        const int mb = rh + 2 * i;
         if (mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
@@ -408,20 +446,20 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = gelu_erf(acc[4 * q + e] + bv[e]);
-          store_h4(Qt, mb * 32 + rl, 32 * w + 8 * q + 4 * g, v);
+          store_h4(Qt, mb * 32 + rl, 32 * wc + 8 * q + 4 * g, v);
         }
       }
     }
-    if (l + 1 < p.L) {
-      load_wq(l + 1);
-      vec_store((l + 1) & 1);  // layer l+1's vectors (its LN1 runs below)
-    }
+    if (l + 1 < p.L) vec_store((l + 1) & 1);  // layer l+1's vectors (its LN1 runs below)
     lds_sync();  // u complete
+    if (l + 1 < p.L) load_wq(l + 1, 0);
     // ---- x += u . W_2^T + b_2 ----
     {
-      const f32x4* b24 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B2 + 32 * w + 4 * g);
+      refresh();
+      const f32x4* b24 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B2 + 32 * wc + 4 * g);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+      for (int i = 0; i < 2; ++i) {
+        const int mb = rh + 2 * i;
         if (mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
@@ -431,7 +469,7 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
         for (int q = 0; q < 4; ++q) {
           const f32x4 bv = b24[2 * q];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) xr[mb][4 * q + e] = xr[mb][4 * q + e] + (acc[4 * q + e] + bv[e]);
+          for (int e = 0; e < 4; ++e) xr[i][4 * q + e] = xr[i][4 * q + e] + (acc[4 * q + e] + bv[e]);
         }
       }
     }
@@ -445,7 +483,10 @@ __global__ __launch_bounds__(256, 1) void small_forward_kernel(SmallArgs p) {
 
 template <int HDP, bool CAUSAL>
 int launch_small(const SmallArgs& p, int64_t batch, hipStream_t st) {
-  hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, CAUSAL>), dim3((unsigned)batch), dim3(256), 0, st, p);
+  // 8 waves: column block w & 3, row blocks (w >> 2) + {0, 2}.  A single row
+  // block (S <= 32) leaves waves 4-7 without rows: 4 waves then.
+  const unsigned threads = p.S <= 32 ? 256 : 512;
+  hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, CAUSAL>), dim3((unsigned)batch), dim3(threads), 0, st, p);
   return check_launch("tk_small_forward");
 }
 
