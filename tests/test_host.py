@@ -236,6 +236,9 @@ def test_hot_kernels_use_no_scratch():
     assert len(hd128) == 12
     hot += hd128
     hot += [k for k in usage if "flash_generic_kernel" in k]
+    # every attention instantiation (head dims 16-256, masked or not)
+    hot += [k for k in usage if "flash_" in k and k not in hot]
+    assert any("flash_generic_kernelILi256E" in k and "ELb1EEEv" in k for k in hot)  # the head_dim-256 vector path
     hot.append(SMALL_FORWARD_C1)
     small = [k for k in usage if "small_forward_kernel" in k and SMALL_FORWARD_HD128 not in k]
     assert len(small) == 6  # head dims 16, 32, 64, causal and not

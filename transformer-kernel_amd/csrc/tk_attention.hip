@@ -15,13 +15,12 @@
 //     the keys {16t + 8*e2 + 4g + e10} (g = lane >> 5).
 //
 // Two bodies, picked by head_dim at compile time:
-//   flash_dma_body (head_dim <= 64, and 256): K and V tiles copied global -> LDS
+//   flash_dma_body (head_dim <= 64): K and V tiles copied global -> LDS
 //     directly (global_load_lds_dwordx4, row-major); the V^T operand is two
 //     ds_read_b64_tr_b16 of the row-major V tile.  The O^T MFMAs of tile t-1
 //     are deferred into step t, so every MFMA of a step is independent of
 //     the step's exponentials and interleaves with them; the row max of the
-//     next tile is computed in the same pass.  At head_dim 256 (one wave per
-//     SIMD, 4-wave workgroups) tile t's O^T MFMAs run at the end of step t.
+//     next tile is computed in the same pass.
 //   flash_vreg_body (head_dim 128): the deferred P needs 16 more registers
 //     than two waves per SIMD leave at head_dim 128, so tile t's O^T MFMAs
 //     follow its exponentials; V^T is written to LDS from registers with
@@ -91,13 +90,10 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   constexpr int KSTEPS = HD / 16;          // k16 steps of S^T = K.Q^T
   constexpr int NS = 2 * KSTEPS;           // S^T MFMAs per tile
   constexpr int NP = 4 * DB;               // O^T MFMAs per tile
-  // head_dim <= 64: the O^T MFMAs of tile t-1 are deferred into step t (V
-  // tiles t-1, t, t+1 in LDS).  head_dim 256 (one wave per SIMD, no room for
-  // the pending P's operands beside a 256-wide O accumulator) runs tile t's
-  // O^T MFMAs at the end of step t (V tiles t, t+1).
-  constexpr bool DEFER = HD <= 64;
-  constexpr int kVSlots = DEFER ? 3 : 2;
-  constexpr int NM = NS + (DEFER ? NP : 0);  // MFMAs of the interleaved chunk region
+  // The O^T MFMAs of tile t-1 are deferred into step t (V tiles t-1, t, t+1
+  // in LDS).
+  constexpr int kVSlots = 3;
+  constexpr int NM = NS + NP;  // MFMAs of the interleaved chunk region
   constexpr int NC = NM / 2 < 4 ? 4 : NM / 2;  // chunks per step
   constexpr int EPC = 32 / NC;             // score entries per lane per chunk
   // chunk holding the last S^T MFMA, and the first chunk that reads its result
@@ -107,7 +103,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     return c;
   }();
   constexpr int C_MAX = C_LAST_S + 2 < NC ? C_LAST_S + 2 : NC;
-  static_assert(HD <= 64 || HD == 256, "head_dim 128 takes flash_vreg_body");
+  static_assert(HD <= 64, "head_dim 128 takes the ring / pair / register bodies, 256 the generic kernel");
   static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
   static_assert(32 % NC == 0 && EPC % 2 == 0, "chunks must split the 32 entries into pairs");
 
@@ -230,7 +226,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
                                             3, 4, 5, 6, 7);
     return d_ok ? f : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   };
-  // O^T += V^T . P^T for a whole tile (the last tile; every tile at head_dim 256).
+  // O^T += V^T . P^T for a whole tile (the last tile).
   auto pv_all = [&](const f16x8 (&pf)[4], const char* vs_) {
 #pragma unroll
     for (int c = 0; c < NP; ++c)
@@ -288,7 +284,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     // the end of the step, after the deferred MFMAs have added tile kt-1 at
     // the old reference, so no MFMA writes O on a conditional path (an MFMA
     // accumulator written on two paths is copied between register sets on
-    // every step); without deferral (head_dim 256) it is rescaled here.
+    // every step).
     const bool rescale = __any(m_tile > m_run + 8.0f);
     float alpha = 1.0f;
     if (rescale) {
@@ -296,12 +292,6 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
-      if constexpr (!DEFER) {  // no pending P: O is rescaled here (fewer spills at head_dim 256)
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
-      }
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
@@ -313,7 +303,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       if (m < NS) {
         if (HAS_NEXT) frag[m] = read_k(ks_n, m);
       } else if (m < NM) {
-        if (DEFER && HAS_PREV) frag[m] = read_v(vs_p, m - NS);
+        if (HAS_PREV) frag[m] = read_v(vs_p, m - NS);
       }
     };
     auto do_mfma = [&](int m) {
@@ -323,7 +313,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
           s_next[kb2] =
               __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], qf[kk], kk == 0 ? f32x16{} : s_next[kb2], 0, 0, 0);
         }
-      } else if (DEFER && HAS_PREV) {
+      } else if (HAS_PREV) {
         const int c = m - NS;
         acc_o[c % DB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag[m], p_prev[c / DB], acc_o[c % DB], 0, 0, 0);
       }
@@ -377,13 +367,12 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     }
     mx_next = mxn;
     l_run += ls;
-    if (DEFER && rescale) {
+    if (rescale) {
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[d][r] *= alpha;
     }
-    if (!DEFER) pv_all(p_cur, vslot(kt % kVSlots));
     // keep the copy wait after every MFMA and read of the step
     __builtin_amdgcn_sched_barrier(0);
     wait_copies();
@@ -415,31 +404,24 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   const BoolC<false> F{};
   if (n_kt == 1) {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, F);
-    if (DEFER) pv_all(pf_a, vslot(0));
+    pv_all(pf_a, vslot(0));
   } else {
     step(0, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, F);
-    if constexpr (DEFER) {
-      // Two steps per iteration with no branch between them: the loop-carried
-      // accumulators then keep one register assignment.
-      int kt = 1;
-      for (; kt + 1 < n_kt - 1; kt += 2) {
-        step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
-        step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
-      }
-      if (kt < n_kt - 1) step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
-    } else {  // head_dim 256: this shape spills less there
-      for (int kt = 1; kt < n_kt - 1; kt += 2) {
-        step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
-        if (kt + 1 < n_kt - 1) step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
-      }
+    // Two steps per iteration with no branch between them: the loop-carried
+    // accumulators then keep one register assignment.
+    int kt = 1;
+    for (; kt + 1 < n_kt - 1; kt += 2) {
+      step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
+      step(kt + 1, s_a, s_b, pf_a, pf_b, mx_a, mx_b, T, T);
     }
+    if (kt < n_kt - 1) step(kt, s_b, s_a, pf_b, pf_a, mx_b, mx_a, T, T);
     const int kl = n_kt - 1;
     if (kl & 1) {
       step(kl, s_b, s_a, pf_b, pf_a, mx_b, mx_a, F, T);
-      if (DEFER) pv_all(pf_b, vslot(kl % kVSlots));
+      pv_all(pf_b, vslot(kl % kVSlots));
     } else {
       step(kl, s_a, s_b, pf_a, pf_b, mx_a, mx_b, F, T);
-      if (DEFER) pv_all(pf_a, vslot(kl % kVSlots));
+      pv_all(pf_a, vslot(kl % kVSlots));
     }
   }
 
@@ -1468,7 +1450,10 @@ __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
 // one 64-key tile at a time through registers into the flash_dma_body LDS
 // layouts (K chunk-swizzled, V for the transposed reads), exact online
 // softmax (the running max moves with every tile), O stored element-wise.
-template <int HDP, bool CAUSAL, bool KMASK>
+// VEC (hd == HDP, 16-byte q/k/v rows, 8-byte out rows): the same loop with
+// 16-byte Q/K/V loads and 8-byte O stores -- the head_dim-256 path, where
+// this plain loop fits its registers (one wave per SIMD, no spill).
+template <int HDP, bool CAUSAL, bool KMASK, bool VEC>
 __global__ __launch_bounds__(256) void flash_generic_kernel(AttnArgs p, int hd) {
   constexpr int NW = 4, BM = 32 * NW, NT = 64 * NW;
   constexpr int RB = HDP * 2;              // K / V tile row bytes
@@ -1500,12 +1485,18 @@ __global__ __launch_bounds__(256) void flash_generic_kernel(AttnArgs p, int hd) 
 
   f16x8 qf[KSTEPS];
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk)
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    if constexpr (VEC) {
+      qf[kk] = my_row < p.S ? *reinterpret_cast<const f16x8*>(qb + (int64_t)my_row * p.qs[2] + kk * 16 + g * 8)
+                            : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int col = kk * 16 + g * 8 + e;
-      qf[kk][e] = (my_row < p.S && col < hd) ? qb[(int64_t)my_row * p.qs[2] + col] : (f16)0;
+      for (int e = 0; e < 8; ++e) {
+        const int col = kk * 16 + g * 8 + e;
+        qf[kk][e] = (my_row < p.S && col < hd) ? qb[(int64_t)my_row * p.qs[2] + col] : (f16)0;
+      }
     }
+  }
 
   f32x16 acc_o[DB];
 #pragma unroll
@@ -1540,12 +1531,20 @@ __global__ __launch_bounds__(256) void flash_generic_kernel(AttnArgs p, int hd) 
         const int row = idx / CPR, ch = idx % CPR;
         const int key = k0 + row;
         f16x8 kv8, vv8;
+        if constexpr (VEC) {
+          kv8 = vv8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+          if (key < p.S) {
+            kv8 = *reinterpret_cast<const f16x8*>(kb + (int64_t)key * p.ks[2] + ch * 8);
+            vv8 = *reinterpret_cast<const f16x8*>(vb + (int64_t)key * p.vs[2] + ch * 8);
+          }
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int col = ch * 8 + e;
-          const bool in = key < p.S && col < hd;
-          kv8[e] = in ? kb[(int64_t)key * p.ks[2] + col] : (f16)0;
-          vv8[e] = in ? vb[(int64_t)key * p.vs[2] + col] : (f16)0;
+          for (int e = 0; e < 8; ++e) {
+            const int col = ch * 8 + e;
+            const bool in = key < p.S && col < hd;
+            kv8[e] = in ? kb[(int64_t)key * p.ks[2] + col] : (f16)0;
+            vv8[e] = in ? vb[(int64_t)key * p.vs[2] + col] : (f16)0;
+          }
         }
         *reinterpret_cast<f16x8*>(ks_ + swz_off<RB>(row, ch)) = kv8;
         *reinterpret_cast<f16x8*>(vs_ + row * RB + ((ch ^ vswz<RB>(row)) << 4)) = vv8;
@@ -1609,26 +1608,33 @@ __global__ __launch_bounds__(256) void flash_generic_kernel(AttnArgs p, int hd) 
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dd = d * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (dd < hd) ob[dd] = (f16)(acc_o[d][r] * inv);
+      for (int r = 0; r < 16; r += 4) {
+        const int dd = d * 32 + 8 * (r >> 2) + 4 * g;
+        if constexpr (VEC) {
+          *reinterpret_cast<f16x4*>(ob + dd) = f16x4{(f16)(acc_o[d][r] * inv), (f16)(acc_o[d][r + 1] * inv),
+                                                     (f16)(acc_o[d][r + 2] * inv), (f16)(acc_o[d][r + 3] * inv)};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (dd + e < hd) ob[dd + e] = (f16)(acc_o[d][r + e] * inv);
+        }
       }
   }
 }
 
-template <int HDP>
+template <int HDP, bool VEC = false>
 int launch_generic(const AttnArgs& p, int hd, bool causal, hipStream_t st) {
   const int64_t grid = (int64_t)((p.S + 127) / 128) * p.B * p.H;
   const dim3 g((unsigned)grid), blk(256);
   const bool km = p.kv != nullptr;
   if (causal && km)
-    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, true>), g, blk, 0, st, p, hd);
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, true, VEC>), g, blk, 0, st, p, hd);
   else if (causal)
-    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, false>), g, blk, 0, st, p, hd);
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, true, false, VEC>), g, blk, 0, st, p, hd);
   else if (km)
-    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, true>), g, blk, 0, st, p, hd);
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, true, VEC>), g, blk, 0, st, p, hd);
   else
-    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, false>), g, blk, 0, st, p, hd);
+    hipLaunchKernelGGL((flash_generic_kernel<HDP, false, false, VEC>), g, blk, 0, st, p, hd);
   return check_launch("tk_flash_attn_fwd");
 }
 
@@ -1703,15 +1709,11 @@ int launch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
 constexpr int kLongS = 32768;
 template <int HD>
 int dispatch_flash(const AttnArgs& p, bool causal, hipStream_t st) {
-  if constexpr (HD == 256) {  // one wave per SIMD: at most four waves (128 rows)
-    if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
-  } else {
-    if (p.S > 128) {
-      if (HD <= 64 && p.S <= kLongS) return launch_flash<HD, 4>(p, causal, st);
-      return launch_flash<HD, 8>(p, causal, st);
-    }
-    if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
+  if (p.S > 128) {
+    if (HD <= 64 && p.S <= kLongS) return launch_flash<HD, 4>(p, causal, st);
+    return launch_flash<HD, 8>(p, causal, st);
   }
+  if (p.S > 64) return launch_flash<HD, 4>(p, causal, st);
   if constexpr (HD <= 64) return launch_single<HD>(p, causal, st);
   else return launch_flash<HD, 2>(p, causal, st);
 }
@@ -1782,7 +1784,10 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
       case 32: return dispatch_flash<32>(p, c, st);
       case 64: return dispatch_flash<64>(p, c, st);
       case 128: return dispatch_flash<128>(p, c, st);
-      default: return dispatch_flash<256>(p, c, st);
+      // head_dim 256: the generic kernel's plain tile loop on 16-byte rows
+      // (appendix case 8, b64 s128: 41 -> 29 us against a DMA-ring body
+      // that spilled 0.5-2.6 KB per lane at this width)
+      default: return launch_generic<256, true>(p, 256, c, st);
     }
   }
   const int hd = (int)head_dim;
