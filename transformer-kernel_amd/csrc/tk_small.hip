@@ -310,7 +310,9 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
         }
       }
     }
-    load_wo(l);
+    // W_o's fragments load under the attention phase; at head_dim 128 its
+    // 64-register O leaves no room for them, so they follow it.
+    if constexpr (HDP < 128) load_wo(l);
     if (l + 1 < p.L) vec_load(l + 1);
     lds_sync();  // Q, K, V complete
     // ---- attention over this wave's (head, query block) items; ctx -> h tile ----
@@ -322,9 +324,14 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       const int hh = k % p.H;
       const int hc = hh * HDP / 8;  // first chunk of this head's columns
       const int row = qb * 32 + rl;
-      f16x8 qf[HK];
+      // Q^T fragments: held in registers for the item, or at head_dim 128
+      // (32 registers beside a 64-register O) re-read from LDS per key block.
+      constexpr bool Q_REG = HK < 8;
+      f16x8 qf[Q_REG ? HK : 1];
+      if constexpr (Q_REG) {
 #pragma unroll
-      for (int kk = 0; kk < HK; ++kk) qf[kk] = afrag(Qt, row, hc, kk);
+        for (int kk = 0; kk < HK; ++kk) qf[kk] = afrag(Qt, row, hc, kk);
+      }
       const int kb_end = CAUSAL ? qb + 1 : MB;
       // Online softmax over the 32-key blocks (S^T = K . Q^T: a lane holds 16
       // keys of query `row`, its partner lane the other 16): running max m_run
@@ -341,7 +348,8 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
           f32x16 a = {};
 #pragma unroll
           for (int kk = 0; kk < HK; ++kk)
-            a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk), qf[kk], a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk),
+                                                       Q_REG ? qf[Q_REG ? kk : 0] : afrag(Qt, row, hc, kk), a, 0, 0, 0);
           float mx = -INFINITY;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -403,6 +411,7 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
           }
         }
     }
+    if constexpr (HDP == 128) load_wo(l);
     load_w1(l);
     lds_sync();  // ctx complete
     // ---- x += ctx . W_o^T + b_o ----
