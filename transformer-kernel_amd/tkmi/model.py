@@ -141,6 +141,7 @@ class OptimizedTransformer(BaselineTransformer):
         self.head_dim_padded = _padded_head_dim(self.head_dim)
         self._weight_cache: Optional[List[_LayerWeights]] = None
         self._weight_cache_key: Optional[tuple] = None
+        self._param_list: Optional[list] = None  # walking the module tree costs ~60 us per forward
         self._stacked: Optional[dict] = None
         self._small_ok: dict = {}  # seq -> tk_small_forward_supported
         self._dense_mask_ref: Optional[weakref.ReferenceType] = None
@@ -152,6 +153,7 @@ class OptimizedTransformer(BaselineTransformer):
         result = super()._apply(*args, **kwargs)
         self._weight_cache = None
         self._weight_cache_key = None
+        self._param_list = None
         return result
 
     def _weights(self) -> List[_LayerWeights]:
@@ -159,8 +161,14 @@ class OptimizedTransformer(BaselineTransformer):
 
         The key includes every parameter's version counter, so an in-place
         update (``load_state_dict`` after a forward) invalidates the cache.
+        The parameter list itself is cached (dropped with the packed weights in
+        ``_apply``): replacing a Parameter object by attribute assignment after
+        a forward is not seen -- the reference's cache sees neither that nor
+        in-place updates (src/optimized.py:265-285).
         """
-        params = list(self.parameters())
+        params = self._param_list
+        if params is None:
+            params = self._param_list = list(self.parameters())
         key = (params[0].device, sum(p._version for p in params), len(params))
         if self._weight_cache is not None and self._weight_cache_key == key:
             return self._weight_cache
