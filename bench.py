@@ -368,6 +368,11 @@ def main() -> int:
         "frac": dom["frac"],
         "traffic": measured_traffic(workload, dom_name) if args.dtype == "float32" else None,
     }
+    if roofline["traffic"] is not None:
+        # a process cannot count its own dispatches' bytes; the figure is the
+        # committed counter run of this same command
+        roofline["traffic_source"] = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over "
+                                      "this bench command, scaled by a plain-copy calibration (x2.0, x1.0)")
 
     cpu, parity = None, None
     if not args.no_cpu_baseline:
