@@ -354,7 +354,9 @@ def _attention_ref_keymask(q, k, v, scale, causal, key_valid):
     return torch.matmul(probs, v.float()).transpose(1, 2).reshape(b, s, h * hd)
 
 
-@pytest.mark.parametrize("shape", [(2, 4, 128, 32), (3, 2, 100, 64), (2, 2, 700, 128), (1, 2, 64, 16)],
+@pytest.mark.parametrize("shape", [(2, 4, 128, 32), (3, 2, 100, 64), (2, 2, 700, 128), (1, 2, 64, 16),
+                                   (1, 2, 300, 256), (2, 1, 64, 256),  # head_dim 256 (generic vector kernel)
+                                   (2, 2, 90, 48)],                    # element-load kernel
                          ids=lambda s: "b{}h{}s{}d{}".format(*s))
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
 def test_flash_attention_key_mask(shape, causal):

@@ -219,6 +219,8 @@ PADDED_CASES = [  # (B, S, D, H, F, L, causal), padding ratio
     ((2, 96, 512, 8, 1024, 2, True), 0.4),    # residual GEMM + standalone LayerNorm (d_model 512)
     ((2, 600, 256, 4, 512, 1, False), 0.5),   # 8-wave attention tiles, ragged S
     ((2, 130, 64, 4, 128, 2, True), 0.8),     # heavy padding
+    ((2, 200, 256, 2, 256, 1, False), 0.3),   # head_dim 128
+    ((2, 130, 512, 2, 512, 1, True), 0.4),    # head_dim 256
 ]
 
 
