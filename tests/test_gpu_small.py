@@ -31,6 +31,9 @@ SHAPES = [
     (2, 100, 128, 8, 128, 2, True),    # head_dim 16
     (2, 128, 128, 4, 128, 1, False),
     (1, 1, 128, 4, 128, 2, True),      # one token
+    (2, 50, 128, 4, 128, 2, True),     # two row blocks: waves 4-7 own one valid block
+    (3, 64, 128, 2, 128, 2, False),
+    (2, 96, 128, 1, 128, 1, True),     # three row blocks, head_dim 128
 ]
 
 
