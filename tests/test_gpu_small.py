@@ -5,7 +5,9 @@ width 128 with head_dim 16/32/64/128, causal and not) against
   * the CPU oracle, with the harness's rule |d| <= 0.002 or |d| <= 0.02|ref|
     (src/torch_transformer_benchmark.py:309-316);
   * the layer-by-layer HIP path on the same weights and input (same
-    numerics, different fp16 rounding points in LayerNorm sums: within 2e-3).
+    arithmetic, different fp16 rounding points -- LayerNorm sums, and P
+    rounded per 32-key block here against the layer path's key tiles:
+    within 2e-3).
 A padded input, and a shape outside the envelope, take the layer path.
 """
 
