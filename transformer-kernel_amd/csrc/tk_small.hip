@@ -351,11 +351,16 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
             a = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(Kt, kb * 32 + rl, hc, kk),
                                                        Q_REG ? qf[Q_REG ? kk : 0] : afrag(Qt, row, hc, kk), a, 0, 0, 0);
           float mx = -INFINITY;
+          if ((CAUSAL && kb == qb) || kb * 32 + 32 > S) {  // the diagonal block, the block holding key S-1
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= S || (CAUSAL && key > row)) a[r] = -INFINITY;
-            mx = fmaxf(mx, a[r]);
+            for (int r = 0; r < 16; ++r) {
+              const int key = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+              if (key >= S || (CAUSAL && key > row)) a[r] = -INFINITY;
+              mx = fmaxf(mx, a[r]);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, a[r]);
           }
           const float m_new = fmaxf(m_run, pair_max(mx) * cs);  // cs > 0: max(s)*cs == max(s*cs)
           if (kb > 0) {
