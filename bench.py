@@ -245,7 +245,7 @@ def main() -> int:
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: this build has no multi-GPU path "
-            "(see the sharding section of DESIGN.md); run with --gpus 1",
+            "(collectives, sharding and rank code are not part of it); run with --gpus 1",
             file=sys.stderr,
         )
         return 2

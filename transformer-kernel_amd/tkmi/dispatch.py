@@ -50,7 +50,7 @@ def build_table(paths: Iterable[pathlib.Path]) -> Dict:
         data = json.loads(pathlib.Path(path).read_text())
         if data.get("schema") != 1:
             continue
-        sources.append(str(path))
+        sources.append(pathlib.Path(path).name)
         for rec in data.get("cases", []):
             opt = rec.get("optimized") or {}
             ms = opt.get("median_ms")
@@ -61,7 +61,7 @@ def build_table(paths: Iterable[pathlib.Path]) -> Dict:
                 best[key] = {"shape": {k: rec["case"][k] for k in SHAPE_FIELDS},
                              "settings": settings_of(data.get("passthrough_args", []),
                                                      rec["case"].get("extra_args", [])),
-                             "median_ms": ms, "source": str(path)}
+                             "median_ms": ms, "source": pathlib.Path(path).name}
     return {"schema": 1, "generated_at": time.strftime("%Y-%m-%dT%H:%M:%S%z"), "sources": sources,
             "shapes": sorted(best.values(), key=lambda e: shape_key(e["shape"]))}
 
