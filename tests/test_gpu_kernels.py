@@ -141,6 +141,9 @@ GEMM_SHAPES = [  # one or more per tile configuration of the dispatch, direct an
     (12800, 512, 2048),   # 256x128 tiles, three K stages
     (13000, 500, 2056),   # 256x128 tiles, K tail, M and N tails
     (4100, 4200, 1032),   # 256x256 tiles, K tail, M and N tails
+    (1, 384, 128),        # one row
+    (300, 1, 64),         # one output column
+    (200, 150, 100),      # K not a multiple of 8: element loads, zero fill past K
 ]
 
 
@@ -255,6 +258,11 @@ ATTN_SHAPES = [  # (B, H, S, hd); the reference's shapes (src/test_triton_kernel
     (4, 8, 64, 64),     # C2-like: one key tile per head
     (1, 2, 64, 256),
     (2, 3, 700, 256),   # head_dim 256, 4-wave tiles, ragged last tile
+    (2, 2, 1, 64),      # one key
+    (2, 1, 63, 32),     # one key short of a tile
+    (1, 2, 65, 64),     # one key past the first tile
+    (1, 2, 129, 64),    # past 128 rows: the long-sequence dispatch
+    (1, 2, 129, 128),
 ]
 
 
