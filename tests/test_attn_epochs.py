@@ -1,0 +1,219 @@
+"""The generated steady-state loop of the head_dim-128 causal attention
+(transformer-kernel_amd/csrc/gen_attn_epochs.py -> tk_attn_epochs.inc).
+
+CPU checks of the asm text: it is the generator's output, the kernel's clobber list
+names exactly the registers it uses beyond its operands, it never writes the
+input-only Q fragments, and along every path through the loop (rescale taken or
+skipped, back edge included) the hazards the hardware does not interlock get at
+least the wait states the compiler gives them for gfx950.  The wait-state
+checker is itself checked on planted mistakes.  Bit-identity with the compiled
+epochs is a GPU test (tests/test_gpu_kernels.py).
+"""
+
+from __future__ import annotations
+
+import importlib.util
+import pathlib
+import re
+
+import pytest
+
+CSRC = pathlib.Path(__file__).resolve().parents[1] / "transformer-kernel_amd" / "csrc"
+
+
+def _gen():
+    spec = importlib.util.spec_from_file_location("gen_attn_epochs", CSRC / "gen_attn_epochs.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+gen = _gen()
+
+
+def test_committed_inc_is_the_generator_output():
+    assert (CSRC / "tk_attn_epochs.inc").read_text() == gen.render()
+
+
+def test_kernel_clobber_list_matches_the_generator():
+    src = (CSRC / "tk_attention.hip").read_text()
+    i = src.index('#include "tk_attn_epochs.inc"')
+    stmt = src[i:src.index(");", i)]
+    clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
+    assert clobbers == gen.CLOBBERED
+    for extra in ('"vcc"', '"scc"', '"memory"'):
+        assert extra in stmt
+
+
+# --------------------------------------------------------------------------- #
+# instruction model
+# --------------------------------------------------------------------------- #
+
+
+def _regs(tok: str) -> list[str]:
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return [f"v{r}" for r in range(int(m.group(1)), int(m.group(2)) + 1)]
+    m = re.fullmatch(r"-?v(\d+)", tok)
+    if m:
+        return [f"v{m.group(1)}"]
+    if tok in ("m0", "vcc"):
+        return [tok]
+    return []
+
+
+class Ins:
+    def __init__(self, text: str):
+        self.text = text
+        parts = text.split(None, 1)
+        self.op = parts[0]
+        ops = [t.strip() for t in parts[1].split(",")] if len(parts) > 1 else []
+        ops = [t.split()[0] for t in ops if t]  # drop "offset:..." modifiers
+        self.reads: set[str] = set()
+        self.writes: set[str] = set()
+        self.src_ab: set[str] = set()
+        op = self.op
+        if op.startswith("s_nop"):
+            self.waits = int(ops[0]) + 1
+        else:
+            self.waits = 1
+        if op.startswith("v_mfma"):
+            self.writes = set(_regs(ops[0]))
+            self.src_ab = set(_regs(ops[1])) | set(_regs(ops[2]))
+            self.reads = self.src_ab | set(_regs(ops[3]))
+        elif op.startswith("v_cmp"):
+            self.writes = {"vcc"}
+            self.reads = {r for t in ops[1:] for r in _regs(t)}
+        elif op.startswith("v_permlane32_swap"):
+            self.writes = self.reads = {r for t in ops for r in _regs(t)}
+        elif op.startswith("v_") or op.startswith("ds_read"):
+            self.writes = set(_regs(ops[0]))
+            self.reads = {r for t in ops[1:] for r in _regs(t)}
+            if op.startswith("v_dot2c"):
+                self.reads |= self.writes
+        elif op.startswith("global_load_lds"):
+            self.reads = {"m0"}
+        elif op.startswith("s_") and ops and ops[0] == "m0":
+            self.writes = {"m0"}
+        elif op == "s_cbranch_vccz":
+            self.reads = {"vcc"}
+        self.target = ops[0] if op.startswith("s_cbranch") or op == "s_branch" else None
+
+
+def _cfg(lines: list[str]):
+    """Instructions and the predecessors of each (forward branches, the loop's back edge)."""
+    ins, label_at = [], {}
+    for line in lines:
+        if line.endswith(":"):
+            label_at[line[:-1]] = len(ins)
+        else:
+            ins.append(Ins(line))
+    preds = [set() for _ in ins]
+    for i, x in enumerate(ins):
+        if i + 1 < len(ins) and x.op != "s_branch":
+            preds[i + 1].add(i)
+        if x.target is not None:
+            preds[label_at[x.target]].add(i)
+    return ins, preds
+
+
+def _rule(prod: Ins, cons: Ins, reg: str) -> int:
+    """Wait states needed between a producer writing `reg` and a consumer touching it."""
+    p, c = prod.op, cons.op
+    touches = reg in cons.reads or reg in cons.writes
+    if p.startswith("v_mfma"):
+        if c.startswith("v_mfma"):
+            return 18 if reg in cons.src_ab else 0  # accumulate chains forward
+        return 18 if touches else 0
+    if p.startswith("v_dot2c"):
+        return 3 if touches and c.startswith("v_") and not c.startswith("v_dot2c") else 0
+    if p.startswith("v_exp"):
+        return 1 if reg in cons.reads and c.startswith("v_") and not c.startswith("v_exp") else 0
+    if reg == "m0":
+        return 1 if c.startswith("global_load_lds") else 0
+    if reg == "vcc":
+        return 4 if c == "s_cbranch_vccz" else 0
+    if c.startswith("v_permlane32_swap") and p.startswith("v_"):
+        return 2 if reg in cons.reads else 0
+    return 0
+
+
+def hazard_violations(lines: list[str], horizon: int = 32) -> list[str]:
+    ins, preds = _cfg(lines)
+    bad = []
+    for ci, cons in enumerate(ins):
+        want = cons.reads | cons.writes
+        if not want:
+            continue
+        # backward walk over every path: (instruction, wait states so far, registers not yet shadowed)
+        stack = [(p, 0, frozenset(want)) for p in preds[ci]]
+        seen = set()
+        while stack:
+            pi, ws, regs = stack.pop()
+            if (pi, ws, regs) in seen or ws > horizon or not regs:
+                continue
+            seen.add((pi, ws, regs))
+            prod = ins[pi]
+            hit = regs & prod.writes
+            for reg in hit:
+                need = _rule(prod, cons, reg)
+                if ws < need:
+                    bad.append(f"{prod.text!r} -> {cons.text!r} ({reg}): {ws} < {need}")
+            rest = regs - hit
+            for q in preds[pi]:
+                stack.append((q, ws + prod.waits, rest))
+    return bad
+
+
+def _asm_lines(program: list[str]) -> list[str]:
+    return [l.replace("%=", "0") for l in program]
+
+
+def test_generated_loop_meets_the_wait_states():
+    bad = hazard_violations(_asm_lines(gen.program()))
+    assert not bad, "\n".join(bad[:10])
+
+
+@pytest.mark.parametrize("planted", ["dot2c", "exp", "mfma", "m0", "permlane"])
+def test_wait_state_checker_finds_planted_mistakes(planted):
+    prog = _asm_lines(gen.program())
+    if planted == "dot2c":  # the l_run update right after the last row-sum dot
+        i = next(i for i, l in enumerate(prog) if l.startswith("v_add_f32 v193"))
+        assert prog[i - 1] == "s_nop 2"
+        del prog[i - 1]
+    elif planted == "exp":  # P conversion right after the second exponential
+        i = next(i for i, l in enumerate(prog) if l.startswith("v_cvt_pk_f16_f32"))
+        assert prog[i - 1] == "s_nop 0"
+        del prog[i - 1]
+    elif planted == "mfma":  # row max right after the score MFMAs
+        i = next(i for i, l in enumerate(prog) if l.startswith("v_max3_f32"))
+        del prog[i - 3:i]
+    elif planted == "m0":
+        i = next(i for i, l in enumerate(prog) if l.startswith("global_load_lds"))
+        assert prog[i - 1] == "s_nop 0"
+        del prog[i - 1]
+    else:
+        i = next(i for i, l in enumerate(prog) if l.startswith("v_permlane32_swap"))
+        assert prog[i - 1] == "s_nop 1"
+        del prog[i - 1]
+    assert hazard_violations(prog), planted
+
+
+def test_loop_registers_stay_in_its_operands_and_clobbers():
+    allowed = {f"v{r}" for r in gen.PINNED | set(gen.CLOBBERED)}
+    q_regs = {f"v{r}" for r in range(gen.Q, gen.Q + 32)}
+    ins, _ = _cfg(_asm_lines(gen.program()))
+    used = set()
+    for x in ins:
+        used |= {r for r in x.reads | x.writes if re.fullmatch(r"v\d+", r)}
+        assert not (x.writes & q_regs), x.text  # Q is an input-only operand
+    assert used <= allowed, sorted(used - allowed)
+    # the pinned P region A and O are both read and written; every clobber is used
+    assert {f"v{r}" for r in gen.CLOBBERED} <= used
+
+
+def test_loop_covers_four_epochs_of_32_mfmas():
+    prog = gen.program()
+    assert sum(1 for l in prog if l.startswith("v_mfma")) == 4 * 32
+    assert sum(1 for l in prog if l == "s_barrier") == 4
+    assert sum(1 for l in prog if l.startswith("global_load_lds")) == 4 * 4

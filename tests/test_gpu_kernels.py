@@ -325,6 +325,48 @@ def test_flash_attention_long_ragged(s, hd):
         assert bad == 0, (causal, err)
 
 
+@pytest.mark.parametrize("s", [1024, 1300, 2100])
+def test_flash_attention_epoch_loop_is_bit_identical(s):
+    """head_dim 128, causal: the key tiles below a 256-row query block's diagonal
+    run from the generated asm loop (tk_attn_epochs.inc) when the K/V copy span
+    fits 32-bit offsets.  K/V rows 4 MiB apart put the span past 2^31 bytes for
+    every query block that would use the loop, so the same values take the
+    compiled epochs; the loop changes the instruction order, not the arithmetic,
+    so the two outputs must agree bit for bit (and both with the reference)."""
+    b, h, hd = 1, 1, 128
+    q, k, v = _qkv((b, h, s, hd), seed=s)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    compact = ops.flash_attention(qd, kd, vd, hd ** -0.5, True)
+    rs = 1 << 21  # fp16 elements between K (and V) rows
+    wide_k = torch.zeros(s, rs, dtype=torch.float16, device=DEV)
+    wide_v = torch.zeros(s, rs, dtype=torch.float16, device=DEV)
+    wide_k[:, :hd] = kd[0, 0]
+    wide_v[:, :hd] = vd[0, 0]
+    kw, vw = wide_k[:, :hd][None, None], wide_v[:, :hd][None, None]
+    assert kw.stride(2) == rs and torch.equal(kw, kd)
+    spread = ops.flash_attention(qd, kw, vw, hd ** -0.5, True)
+    del wide_k, wide_v
+    assert torch.equal(compact, spread)
+    bad, err = or_rule_violations(compact, ob.attention_ref(q, k, v, hd ** -0.5, True))
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_flash_attention_v_rows_8_byte_aligned(causal):
+    """head_dim 128 with V rows only 8-byte aligned: the non-causal body loads V
+    8 bytes at a time, the causal bodies copy 16-byte chunks and must not get it
+    (such calls take the element-load kernel)."""
+    b, h, s, hd = 1, 2, 300, 128
+    q, k, v = _qkv((b, h, s, hd), seed=11)
+    vbuf = torch.zeros(b, h, s, hd + 8, dtype=torch.float16, device=DEV)
+    vbuf[..., 4:4 + hd] = v.to(DEV)
+    vv = vbuf[..., 4:4 + hd]
+    assert vv.data_ptr() % 16 == 8 and torch.equal(vv.cpu(), v)
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), vv, hd ** -0.5, causal)
+    bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+    assert bad == 0, err
+
+
 @pytest.mark.parametrize("hd", [64, 128])
 def test_flash_attention_long_strided_views(hd):
     """q/k/v as strided views of one fused [B, S, 3, H, hd] projection, as the model passes them."""

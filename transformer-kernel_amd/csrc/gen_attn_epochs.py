@@ -1,0 +1,215 @@
+"""Emit tk_attn_epochs.inc: the hand-ordered steady-state epochs of the head_dim-128 causal
+attention (flash_pair_body in tk_attention.hip, 8 waves, 256 query rows per workgroup).
+
+    python gen_attn_epochs.py [out.inc]      # default: tk_attn_epochs.inc beside this file
+
+The build runs this before compiling tk_attention.hip, so the .inc and this script cannot drift.
+
+What the loop computes
+----------------------
+Epoch e of the pair body (key tile e = keys 64e .. 64e+63) does, for every wave:
+
+  copies    K tile e+2 into K slot (e+2) % 3, V tile e+1 into V slot (e+1) % 4 (LDS DMA)
+  S phase   S^T(e) = K(e) . Q^T, 16 MFMAs 32x32x16; MFMA c: key block c & 1, k-step c >> 1
+  max       m_tile = scale*log2(e) * max over the lane pair; lazy rescale when any lane's
+            m_tile exceeds m_run + 8: m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new),
+            l_run *= alpha
+  P.V phase O^T += V^T(e-1) . P^T(e-1), 16 MFMAs (head-dim block c & 3, P block c >> 2),
+            with P(e) = fp16(exp2(s * cs - m_run)) and its fp16 row sum (dot2 with 1.0h)
+            computed between them
+  rescale   O *= alpha when the rescale ran
+  end       wait for the previous epoch's copies, barrier
+
+Each lane performs the same operations on the same operands in the same order as the compiled
+epoch, so the results are bit-identical to it.  The loop covers the epochs [1, 1 + 4*groups),
+which the host side chooses so that no key tile in them needs a causal or length mask (every key
+is below every query row of the workgroup) and no copy is clamped to the last tile; m_run is
+finite there (epoch 0 saw key 0), so the -inf guards of the compiled epoch are not needed.
+
+One loop iteration is 4 epochs, so epoch e = 1 + 4i + u (loop position u) reads V(e-1) from
+V slot (e-1) % 4 = u and writes V(e+1) into slot (u + 2) % 4: both are immediate LDS offsets.
+The K ring has 3 slots, so its read and write slots rotate through the SGPR trackers krd and kwr
+(byte offsets of the slots, starting at slots 1 and 0 for epoch 1).
+
+Register map (all VGPRs; the asm statement pins or clobbers every one of them)
+-------------------------------------------------------------------------------
+  v[64:127]   O^T accumulators, 4 x 16          (in/out)
+  v[128:159]  Q fragments, 8 x 4                 (in)
+  v[160:175]  P tile region A                     (in/out: holds P(e-1) at entry and exit)
+  v[176:191]  P tile region B                     (clobbered)
+  v192, v193  m_run, l_run                        (in/out)
+  v194..v197  T0, T1, ALPHA, LS (row-sum partial) (clobbered); MX = T0 and TMP = T1 (the S and
+              max phases use MX/TMP, the P.V phase T0/T1)
+  v[198:213]  scores, key block 1                 (clobbered)
+  v[214:225]  operand ring, 3 x 4: K fragments in the S phase, V fragments in the P.V phase
+Scores of key block 0 live in the region that receives the new P tile: P.V step c writes P
+register c after reading scores 2c and 2c+1, and score c was read at step c // 2.  Regions A and
+B alternate between "P being consumed" and "scores block 0 / new P" from epoch to epoch.
+
+Wait states given for the hazards the hardware does not interlock (each at least what the
+compiler inserts for gfx950 in the same situation)
+------------------------------------------------------------------------------------------
+  SALU write of M0 -> LDS DMA reading M0                1   (s_nop 0)
+  MFMA 32x32 result -> VALU read or write               24  (3 x s_nop 7)
+  VALU write       -> v_permlane32_swap read            2   (s_nop 1)
+  VALU write VCC   -> s_cbranch_vccz                    4   (s_nop 3)
+  v_exp (trans.)   -> non-trans. VALU read              1   (s_nop 0)
+  v_dot2c result   -> different VALU read               3   (s_nop 2)
+  MFMA accumulate chains and same-opcode v_dot2c accumulate chains need none.
+"""
+from __future__ import annotations
+
+import pathlib
+import sys
+
+O = 64                # v[64:127]  O^T accumulators, 4 x 16
+Q = 128               # v[128:159] Q fragments, 8 x 4
+P = (160, 176)        # the two 16-register P regions
+MR, LR = 192, 193     # m_run, l_run
+T0, T1, ALPHA, LS = 194, 195, 196, 197
+MX, TMP = T0, T1
+SB1 = 198             # v[198:213] scores, key block 1
+RING = 214            # v[214:225] K (S phase) / V (P.V phase) fragment ring
+TILE = 16384          # bytes per K or V tile in LDS (64 rows x 256 bytes)
+
+PINNED = set(range(64, 176)) | {MR, LR}               # operands of the asm statement
+CLOBBERED = sorted(set(range(176, 192)) | set(range(194, 226)))
+
+
+def v(a: int, n: int = 1) -> str:
+    return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
+
+
+def epoch(u: int) -> list[str]:
+    """Instructions of the epoch at loop position u (0..3)."""
+    pp, pc = (P[0], P[1]) if u % 2 == 0 else (P[1], P[0])
+    sb = (pc, SB1)  # scores: key block 0 in the new-P region, key block 1 in SB1
+
+    def sr(i: int) -> int:  # register of score i (0..31) = accumulator entry i & 15 of block i >> 4
+        return sb[i >> 4] + (i & 15)
+
+    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    # ---- copies: K(e+2) into the K slot kwr, V(e+1) into V slot (u + 2) % 4 ----
+    L += ["s_add_u32 m0, %[ldsw], %[kwr]", "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
+          "s_add_u32 m0, m0, 8192", "s_nop 0", "global_load_lds_dwordx4 %[ko1], %[kb]"]
+    vw = (3 + (u + 2) % 4) * TILE
+    L += [f"s_add_u32 m0, %[ldsw], {vw}", "s_nop 0", "global_load_lds_dwordx4 %[vo0], %[vb]",
+          f"s_add_u32 m0, %[ldsw], {vw + 8192}", "s_nop 0", "global_load_lds_dwordx4 %[vo1], %[vb]"]
+    L += ["v_add_u32 %[ko0], %[kt2], %[ko0]", "v_add_u32 %[ko1], %[kt2], %[ko1]",
+          "v_add_u32 %[vo0], %[vt2], %[vo0]", "v_add_u32 %[vo1], %[vt2], %[vo1]"]
+
+    # ---- S phase: fragment reads run two MFMAs ahead through the 3-entry ring ----
+    def kread(c: int) -> list[str]:
+        # k-step kk reads chunk 2kk + g of the XOR-swizzled row: row offset kl0 ^ (kk << 5)
+        out = []
+        if c % 2 == 0:
+            kk = c >> 1
+            if kk == 0:
+                out.append(f"v_add_u32 {v(TMP)}, %[krd], %[kl0]")
+            else:
+                out += [f"v_xor_b32 {v(TMP)}, {kk << 5}, %[kl0]", f"v_add_u32 {v(TMP)}, %[krd], {v(TMP)}"]
+        out.append(f"ds_read_b128 {v(RING + 4 * (c % 3), 4)}, {v(TMP)} offset:{(c & 1) * 8192}")
+        return out
+
+    L += kread(0) + kread(1)
+    for c in range(16):
+        if c + 2 < 16:
+            L += kread(c + 2)
+        L.append(f"s_waitcnt lgkmcnt({min(2, 15 - c)})")
+        src_c = "0" if (c >> 1) == 0 else v(sb[c & 1], 16)
+        L.append(f"v_mfma_f32_32x32x16_f16 {v(sb[c & 1], 16)}, {v(RING + 4 * (c % 3), 4)}, "
+                 f"{v(Q + 4 * (c >> 1), 4)}, {src_c}")
+
+    # ---- row max over the lane pair, lazy rescale ----
+    L += ["s_nop 7", "s_nop 7", "s_nop 7"]
+    L.append(f"v_max3_f32 {v(MX)}, {v(sr(0))}, {v(sr(1))}, {v(sr(2))}")
+    k = 3
+    while k + 1 < 32:
+        L.append(f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(k))}, {v(sr(k + 1))}")
+        k += 2
+    if k < 32:
+        L.append(f"v_max_f32 {v(MX)}, {v(MX)}, {v(sr(k))}")
+    L += [f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1", f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
+          f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
+          f"v_mul_f32 {v(MX)}, %[cs], {v(MX)}",                 # m_tile
+          f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",            # m_run + 8
+          f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
+          f"s_cbranch_vccz L_norescale_{u}_%="]
+    L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",               # m_new
+          f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
+          f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
+          f"v_mov_b32 {v(MR)}, {v(TMP)}", "s_nop 0",
+          f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
+          "s_mov_b32 %[flag], 1"]
+    L += [f"L_norescale_{u}_%=:"]
+
+    # ---- P.V phase: O^T += V^T(e-1) P^T(e-1); exponentials of S(e) between the MFMAs ----
+    vslot = u * TILE
+
+    def vread(c: int) -> list[str]:
+        t, d = c >> 2, c & 3
+        base = RING + 4 * (c % 3)
+        # the second half-fragment sits 8 tile rows (2048 bytes) further, same swizzle
+        return [f"ds_read_b64_tr_b16 {v(base, 2)}, %[vl{d}] offset:{vslot + t * 4096}",
+                f"ds_read_b64_tr_b16 {v(base + 2, 2)}, %[vl{d}] offset:{vslot + t * 4096 + 2048}"]
+
+    L += vread(0) + vread(1)
+    for c in range(16):
+        if c + 2 < 16:
+            L += vread(c + 2)
+        L.append(f"s_waitcnt lgkmcnt({2 * min(2, 15 - c)})")
+        L.append(f"v_mfma_f32_32x32x16_f16 {v(O + 16 * (c & 3), 16)}, {v(RING + 4 * (c % 3), 4)}, "
+                 f"{v(pp + 4 * (c >> 2), 4)}, {v(O + 16 * (c & 3), 16)}")
+        L += [f"v_fma_f32 {v(T0)}, {v(sr(2 * c))}, %[cs], -{v(MR)}",
+              f"v_fma_f32 {v(T1)}, {v(sr(2 * c + 1))}, %[cs], -{v(MR)}",
+              f"v_exp_f32 {v(T0)}, {v(T0)}",
+              f"v_exp_f32 {v(T1)}, {v(T1)}", "s_nop 0",
+              f"v_cvt_pk_f16_f32 {v(pc + c)}, {v(T0)}, {v(T1)}",
+              f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(pc + c)}"]
+    L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
+    # ---- O rescale ----
+    L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{u}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
+    L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(64)]
+    L += [f"L_noscale_{u}_%=:"]
+    # ---- end: this epoch's copies may stay in flight, the previous epoch's have landed ----
+    L += ["s_waitcnt vmcnt(4)", "s_barrier",
+          "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
+          "s_add_u32 %[kwr], %[kwr], 16384", "s_cmp_eq_u32 %[kwr], 49152", "s_cselect_b32 %[kwr], 0, %[kwr]"]
+    return L
+
+
+def program() -> list[str]:
+    """The whole asm body: M0 saved, `groups` iterations of 4 epochs, M0 restored."""
+    L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]",
+         "s_mov_b32 %[krd], %[krd0]", "s_mov_b32 %[kwr], %[kwr0]", "s_nop 1"]
+    L += ["L_epochs_%=:"]
+    for u in range(4):
+        L += epoch(u)
+    L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_epochs_%="]
+    # the compiled code after the statement reads O: MFMA result latency first
+    L += ["s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    return L
+
+
+def render() -> str:
+    head = "// Generated by gen_attn_epochs.py; do not edit.\n"
+    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program())
+    return head + body + "\n"
+
+
+def clobber_list() -> str:
+    return ", ".join(f'"v{r}"' for r in CLOBBERED)
+
+
+def write(path: pathlib.Path | None = None) -> pathlib.Path:
+    path = path or pathlib.Path(__file__).resolve().parent / "tk_attn_epochs.inc"
+    text = render()
+    if not path.exists() or path.read_text() != text:
+        path.write_text(text)
+    return path
+
+
+if __name__ == "__main__":
+    out = write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None)
+    prog = program()
+    print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")

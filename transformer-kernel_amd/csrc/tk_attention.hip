@@ -1122,17 +1122,20 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
   const f16* k_src[CPW];
   const f16* v_src[CPW];
   int k_col[CPW], v_col[CPW];
+  auto copy_setup = [&](int ln) {
 #pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    const int ci = wave + i * NW;
-    const int row = ci * RPC + lane / CPR;
-    const int phys = lane % CPR;
-    c_row[i] = row;
-    k_col[i] = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
-    v_col[i] = (phys ^ vswz<RB>(row)) * 8;
-    k_src[i] = kb + (int64_t)row * p.ks[2] + k_col[i];
-    v_src[i] = vb + (int64_t)row * p.vs[2] + v_col[i];
-  }
+    for (int i = 0; i < CPW; ++i) {
+      const int ci = wave + i * NW;
+      const int row = ci * RPC + ln / CPR;
+      const int phys = ln % CPR;
+      c_row[i] = row;
+      k_col[i] = ((swz_off<RB>(row, phys) - row * RB) >> 4) * 8;  // the XOR is an involution
+      v_col[i] = (phys ^ vswz<RB>(row)) * 8;
+      k_src[i] = kb + (int64_t)row * p.ks[2] + k_col[i];
+      v_src[i] = vb + (int64_t)row * p.vs[2] + v_col[i];
+    }
+  };
+  copy_setup(lane);
   const int64_t k_tile = (int64_t)kBN * p.ks[2], v_tile = (int64_t)kBN * p.vs[2];
   auto copy_tile = [&](const f16* const (&src)[CPW], const f16* base, int64_t rs, int64_t tstride,
                        const int (&col)[CPW], int j, uint32_t dst) {
@@ -1296,6 +1299,72 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
   f32x16 s[2];
   f16x8 pf_a[4], pf_b[4];
   const bool older = wave < NW / 2;
+
+  // ---- hand-ordered steady state (head_dim 128, 8 waves, causal, no key mask) ----
+  // Epochs [1, 1 + 4*groups) run from one asm loop (tk_attn_epochs.inc, made by
+  // gen_attn_epochs.py), in one instruction order for every wave.  Each lane does
+  // the arithmetic of the compiled epoch in the same order, so O, m and l come out
+  // bit-identical; what changes is the schedule (C4 shape b4 h16 s8192: 1239-1253
+  // -> 1137 us in same-box A/B runs).  The epochs it covers need no mask (every
+  // key tile lies below q0, so below every row of the workgroup) and copy only
+  // whole tiles (K tile e+2 <= e_lim+1 < S/kBN), so none of the compiled epoch's
+  // clamps and guards apply.  The copies use 32-bit offsets from the K and V
+  // bases (span check), and the read addresses are formed by XOR on bits 5-7 of
+  // a 256-byte-aligned row offset.
+  int groups = 0;
+  if constexpr (HD == 128 && NW == 8 && CAUSAL && !KMASK) {
+    const int e_lim = min(q0 / kBN, min(n_kt, p.S / kBN) - 2);
+    const int64_t span =
+        ((int64_t)n_kt + 2) * max(k_tile, v_tile) * 2 + (int64_t)kBN * max(p.ks[2], p.vs[2]) * 2;
+    if (e_lim > 1 && span < (1ll << 31) && (lds_base & 255) == 0) groups = (e_lim - 1) / 4;
+  }
+  // Pinned: O^T v[64:127], Q v[128:159], P region A v[160:175] (P(0) in, P(4*groups)
+  // out), m_run v192, l_run v193; the loop's other registers are clobbered.
+  auto run_epochs = [&]() {
+    static_assert(HD == 128 && NW == 8 && KSL == 3 && VSL == 4 && TILE == 16384 && CPW == 2,
+                  "the generated loop's layout");
+    uint32_t vl[DB], ko[CPW], vo[CPW];
+    const uint32_t kl0 = lds_base + swz_off<RB>(lane & 31, g);  // k-step kk: kl0 ^ (kk << 5)
+#pragma unroll
+    for (int d = 0; d < DB; ++d) vl[d] = lds_base + KSL * TILE + v_rd[0][d];  // v_rd[1][d] = +2048
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {  // first copies of the loop: K(3), V(2)
+      ko[i] = (uint32_t)(((int64_t)c_row[i] * p.ks[2] + k_col[i]) * 2 + 3 * k_tile * 2);
+      vo[i] = (uint32_t)(((int64_t)c_row[i] * p.vs[2] + v_col[i]) * 2 + 2 * v_tile * 2);
+    }
+    const uint32_t ldsw = lds_base + wave * 1024;
+    const uint32_t kt2 = (uint32_t)(k_tile * 2), vt2 = (uint32_t)(v_tile * 2);
+    const float cs = p.scale_log2;
+    const uint32_t krd0 = TILE, kwr0 = 0;  // epoch 1 reads K slot 1, writes K(3) into slot 0
+    uint32_t msave, cnt, krd, kwr, flag;
+    asm volatile(
+#include "tk_attn_epochs.inc"
+        : [o0] "+{v[64:79]}"(acc_o[0]), [o1] "+{v[80:95]}"(acc_o[1]), [o2] "+{v[96:111]}"(acc_o[2]),
+          [o3] "+{v[112:127]}"(acc_o[3]), [pa0] "+{v[160:163]}"(pf_a[0]), [pa1] "+{v[164:167]}"(pf_a[1]),
+          [pa2] "+{v[168:171]}"(pf_a[2]), [pa3] "+{v[172:175]}"(pf_a[3]), [mr] "+{v192}"(m_run),
+          [lr] "+{v193}"(l_run), [ko0] "+&v"(ko[0]), [ko1] "+&v"(ko[1]), [vo0] "+&v"(vo[0]),
+          [vo1] "+&v"(vo[1]), [msave] "=&s"(msave), [cnt] "=&s"(cnt), [krd] "=&s"(krd), [kwr] "=&s"(kwr),
+          [flag] "=&s"(flag)
+        : [q0] "{v[128:131]}"(qf[0]), [q1] "{v[132:135]}"(qf[1]), [q2] "{v[136:139]}"(qf[2]),
+          [q3] "{v[140:143]}"(qf[3]), [q4] "{v[144:147]}"(qf[4]), [q5] "{v[148:151]}"(qf[5]),
+          [q6] "{v[152:155]}"(qf[6]), [q7] "{v[156:159]}"(qf[7]), [kl0] "v"(kl0), [vl0] "v"(vl[0]),
+          [vl1] "v"(vl[1]), [vl2] "v"(vl[2]), [vl3] "v"(vl[3]), [kb] "s"(kb), [vb] "s"(vb),
+          [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), [cs] "s"(cs), [groups] "s"(groups),
+          [krd0] "s"(krd0), [kwr0] "s"(kwr0)
+        : "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187",
+          "v188", "v189", "v190", "v191", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201",
+          "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213",
+          "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225",
+          "vcc", "scc", "memory");
+  };
+  // After the loop (or in its place) the copy addresses are rebuilt from an
+  // opaque lane id rather than kept live across it: held there they spill.
+  auto after_epochs = [&]() {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    copy_setup(ln);
+  };
+
   if (older) {
     // epoch e: copies; S(e); max(e); P.V(e-1) with exp(e); O rescale; barrier
     auto epoch = [&](int e, f16x8 (&pc)[4], const f16x8 (&pp)[4]) {
@@ -1308,18 +1377,24 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
       if (rs) scale_o(alpha);
       epoch_end(e, kbn);
     };
-    int e = 0;
+    epoch(0, pf_a, pf_b);
+    int e = 1;
+    if (groups > 0) {
+      run_epochs();
+      e += 4 * groups;
+    }
+    after_epochs();
     for (; e + 1 < n_kt; e += 2) {
-      epoch(e, pf_a, pf_b);
-      epoch(e + 1, pf_b, pf_a);
+      epoch(e, pf_b, pf_a);
+      epoch(e + 1, pf_a, pf_b);
     }
     wait_vmcnt<0>();
     if (e < n_kt) {
-      epoch(e, pf_a, pf_b);
+      epoch(e, pf_b, pf_a);
       wait_vmcnt<0>();
-      pv_only(n_kt - 1, pf_a);
-    } else {
       pv_only(n_kt - 1, pf_b);
+    } else {
+      pv_only(n_kt - 1, pf_a);
     }
   } else {
     // epoch e: copies; P.V(e-1); S(e); max(e); exp(e); O rescale (O holds
@@ -1336,18 +1411,24 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
       if (rs) scale_o(alpha);
       epoch_end(e, kbn);
     };
-    int e = 0;
+    epoch(0, pf_a, pf_b);
+    int e = 1;
+    if (groups > 0) {
+      run_epochs();
+      e += 4 * groups;
+    }
+    after_epochs();
     for (; e + 1 < n_kt; e += 2) {
-      epoch(e, pf_a, pf_b);
-      epoch(e + 1, pf_b, pf_a);
+      epoch(e, pf_b, pf_a);
+      epoch(e + 1, pf_a, pf_b);
     }
     wait_vmcnt<0>();
     if (e < n_kt) {
-      epoch(e, pf_a, pf_b);
+      epoch(e, pf_b, pf_a);
       wait_vmcnt<0>();
-      pv_only(n_kt - 1, pf_a);
-    } else {
       pv_only(n_kt - 1, pf_b);
+    } else {
+      pv_only(n_kt - 1, pf_a);
     }
   }
 
@@ -1772,11 +1853,13 @@ extern "C" int tk_flash_attn_fwd(const tk_half* q, const tk_half* k, const tk_ha
   hipStream_t st = as_stream(stream);
   const bool c = causal != 0;
   // Vector paths: q, k rows 16-byte vectors (register / LDS-DMA copies); v
-  // rows 16-byte vectors where V is DMA-copied (every head dim but 128, whose
-  // body loads V rows 8 bytes at a time); out rows 8-byte vectors.
-  bool vec = native_head_dim(head_dim) && al(q, 16) && al(k, 16) && al(v, head_dim == 128 ? 8 : 16) && al(out, 8);
+  // rows 16-byte vectors where V is DMA-copied (every body but the non-causal
+  // head_dim-128 one, which loads V rows 8 bytes at a time); out rows 8-byte
+  // vectors.
+  const bool v8 = head_dim == 128 && !c;
+  bool vec = native_head_dim(head_dim) && al(q, 16) && al(k, 16) && al(v, v8 ? 8 : 16) && al(out, 8);
   for (int i = 0; i < 3; ++i)
-    vec = vec && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % (head_dim == 128 ? 4 : 8) == 0 &&
+    vec = vec && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % (v8 ? 4 : 8) == 0 &&
           o_strides[i] % 4 == 0;
   if (vec) {
     switch (head_dim) {

@@ -5,7 +5,8 @@
 
 Every ``csrc/*.hip`` file is compiled to an object under
 ``transformer-kernel_amd/_build/`` (in parallel), then linked into
-``transformer-kernel_amd/tkmi/libtkmi.so``.  The flags target gfx950 only.
+``transformer-kernel_amd/tkmi/libtkmi.so``; ``csrc/gen_attn_epochs.py`` first
+rewrites the generated ``csrc/tk_attn_epochs.inc``.  The flags target gfx950 only.
 ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the compiler from
 emitting packed-fp32 VALU instructions (the host pass warns that it does not
 know the feature; that is harmless).
@@ -83,12 +84,23 @@ def _compile(src: pathlib.Path):
     return obj, _resource_usage(proc.stderr)
 
 
+def generate() -> None:
+    """Write the generated kernel sources (the attention steady-state asm loop)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("gen_attn_epochs", CSRC / "gen_attn_epochs.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    mod.write()
+
+
 def build(verbose: bool = True, jobs: int = 0) -> pathlib.Path:
     """Compile all kernels and link libtkmi.so; returns the library path."""
     BUILD_DIR.mkdir(exist_ok=True)
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    generate()
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(_compile, srcs))
