@@ -181,10 +181,11 @@ def test_wait_state_checker_finds_planted_mistakes(planted):
         i = next(i for i, l in enumerate(prog) if l.startswith("v_add_f32 v193"))
         assert prog[i - 1] == "s_nop 2"
         del prog[i - 1]
-    elif planted == "exp":  # P conversion right after the second exponential
+    elif planted == "exp":  # a P conversion right after the exponential it reads
         i = next(i for i, l in enumerate(prog) if l.startswith("v_cvt_pk_f16_f32"))
-        assert prog[i - 1] == "s_nop 0"
-        del prog[i - 1]
+        src = prog[i].split(", ")[-1]
+        j = max(k for k in range(i) if prog[k] == f"v_exp_f32 {src}, {src}")
+        prog.insert(j + 1, prog[i])
     elif planted == "mfma":  # row max right after the score MFMAs
         i = next(i for i, l in enumerate(prog) if l.startswith("v_max3_f32"))
         del prog[i - 3:i]

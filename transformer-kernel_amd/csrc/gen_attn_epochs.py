@@ -42,6 +42,7 @@ Register map (all VGPRs; the asm statement pins or clobbers every one of them)
               max phases use MX/TMP, the P.V phase T0/T1)
   v[198:213]  scores, key block 1                 (clobbered)
   v[214:225]  operand ring, 3 x 4: K fragments in the S phase, V fragments in the P.V phase
+  v[226:227]  second temporary pair of the exponential pipeline (clobbered)
 Scores of key block 0 live in the region that receives the new P tile: P.V step c writes P
 register c after reading scores 2c and 2c+1, and score c was read at step c // 2.  Regions A and
 B alternate between "P being consumed" and "scores block 0 / new P" from epoch to epoch.
@@ -70,10 +71,11 @@ T0, T1, ALPHA, LS = 194, 195, 196, 197
 MX, TMP = T0, T1
 SB1 = 198             # v[198:213] scores, key block 1
 RING = 214            # v[214:225] K (S phase) / V (P.V phase) fragment ring
+TX = 226              # v[226:227] a second exponential pair in flight (P.V phase)
 TILE = 16384          # bytes per K or V tile in LDS (64 rows x 256 bytes)
 
 PINNED = set(range(64, 176)) | {MR, LR}               # operands of the asm statement
-CLOBBERED = sorted(set(range(176, 192)) | set(range(194, 226)))
+CLOBBERED = sorted(set(range(176, 192)) | set(range(194, 228)))
 
 
 def v(a: int, n: int = 1) -> str:
@@ -121,14 +123,15 @@ def epoch(u: int) -> list[str]:
                  f"{v(Q + 4 * (c >> 1), 4)}, {src_c}")
 
     # ---- row max over the lane pair, lazy rescale ----
+    # two interleaved chains (key blocks 0 and 1), so no max waits on the one before it
     L += ["s_nop 7", "s_nop 7", "s_nop 7"]
-    L.append(f"v_max3_f32 {v(MX)}, {v(sr(0))}, {v(sr(1))}, {v(sr(2))}")
-    k = 3
-    while k + 1 < 32:
-        L.append(f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(k))}, {v(sr(k + 1))}")
-        k += 2
-    if k < 32:
-        L.append(f"v_max_f32 {v(MX)}, {v(MX)}, {v(sr(k))}")
+    L += [f"v_max3_f32 {v(MX)}, {v(sr(0))}, {v(sr(1))}, {v(sr(2))}",
+          f"v_max3_f32 {v(TMP)}, {v(sr(16))}, {v(sr(17))}, {v(sr(18))}"]
+    for k in range(3, 15, 2):
+        L += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(k))}, {v(sr(k + 1))}",
+              f"v_max3_f32 {v(TMP)}, {v(TMP)}, {v(sr(16 + k))}, {v(sr(17 + k))}"]
+    L += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(15))}, {v(TMP)}",
+          f"v_max_f32 {v(MX)}, {v(MX)}, {v(sr(31))}"]
     L += [f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1", f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
           f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
           f"v_mul_f32 {v(MX)}, %[cs], {v(MX)}",                 # m_tile
@@ -153,19 +156,36 @@ def epoch(u: int) -> list[str]:
         return [f"ds_read_b64_tr_b16 {v(base, 2)}, %[vl{d}] offset:{vslot + t * 4096}",
                 f"ds_read_b64_tr_b16 {v(base + 2, 2)}, %[vl{d}] offset:{vslot + t * 4096 + 2048}"]
 
-    L += vread(0) + vread(1)
+    # Exponential pair j (scores 2j, 2j+1 -> P register j) runs as a two-stage pipeline
+    # over the MFMA slots: scaled at slot j-1, then at slot j exponentiated, the next pair
+    # scaled, and packed and summed -- the two scalings sit between each exponential and its
+    # pack.  Two temporary pairs alternate; the row sum still adds pairs in order 0..15.
+    tpair = ((T0, T1), (TX, TX + 1))
+
+    def scale(j: int) -> list[str]:
+        a, b = tpair[j % 2]
+        return [f"v_fma_f32 {v(a)}, {v(sr(2 * j))}, %[cs], -{v(MR)}",
+                f"v_fma_f32 {v(b)}, {v(sr(2 * j + 1))}, %[cs], -{v(MR)}"]
+
+    def expo(j: int) -> list[str]:
+        a, b = tpair[j % 2]
+        return [f"v_exp_f32 {v(a)}, {v(a)}", f"v_exp_f32 {v(b)}, {v(b)}"]
+
+    def pack(j: int) -> list[str]:
+        a, b = tpair[j % 2]
+        return [f"v_cvt_pk_f16_f32 {v(pc + j)}, {v(a)}, {v(b)}",
+                f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(pc + j)}"]
+
+    L += vread(0) + vread(1) + scale(0)
     for c in range(16):
         if c + 2 < 16:
             L += vread(c + 2)
         L.append(f"s_waitcnt lgkmcnt({2 * min(2, 15 - c)})")
         L.append(f"v_mfma_f32_32x32x16_f16 {v(O + 16 * (c & 3), 16)}, {v(RING + 4 * (c % 3), 4)}, "
                  f"{v(pp + 4 * (c >> 2), 4)}, {v(O + 16 * (c & 3), 16)}")
-        L += [f"v_fma_f32 {v(T0)}, {v(sr(2 * c))}, %[cs], -{v(MR)}",
-              f"v_fma_f32 {v(T1)}, {v(sr(2 * c + 1))}, %[cs], -{v(MR)}",
-              f"v_exp_f32 {v(T0)}, {v(T0)}",
-              f"v_exp_f32 {v(T1)}, {v(T1)}", "s_nop 0",
-              f"v_cvt_pk_f16_f32 {v(pc + c)}, {v(T0)}, {v(T1)}",
-              f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(pc + c)}"]
+        L += expo(c)
+        L += scale(c + 1) if c + 1 < 16 else ["s_nop 1"]
+        L += pack(c)
     L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
     # ---- O rescale ----
     L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{u}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]

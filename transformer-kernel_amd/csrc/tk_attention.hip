@@ -1355,7 +1355,7 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
           "v188", "v189", "v190", "v191", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201",
           "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213",
           "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225",
-          "vcc", "scc", "memory");
+          "v226", "v227", "vcc", "scc", "memory");
   };
   // After the loop (or in its place) the copy addresses are rebuilt from an
   // opaque lane id rather than kept live across it: held there they spill.
