@@ -1,5 +1,6 @@
-"""The generated steady-state loop of the head_dim-128 causal attention
-(transformer-kernel_amd/csrc/gen_attn_epochs.py -> tk_attn_epochs.inc).
+"""The generated steady-state loops of the causal attention: head_dim 128
+(transformer-kernel_amd/csrc/gen_attn_epochs.py -> tk_attn_epochs.inc) and
+head_dim 64 (gen_attn_steps64.py -> tk_attn_steps64.inc).
 
 CPU checks of the asm text: it is the generator's output, the kernel's clobber list
 names exactly the registers it uses beyond its operands, it never writes the
@@ -21,26 +22,33 @@ import pytest
 CSRC = pathlib.Path(__file__).resolve().parents[1] / "transformer-kernel_amd" / "csrc"
 
 
-def _gen():
-    spec = importlib.util.spec_from_file_location("gen_attn_epochs", CSRC / "gen_attn_epochs.py")
+def _gen(name):
+    spec = importlib.util.spec_from_file_location(name, CSRC / f"{name}.py")
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     return mod
 
 
-gen = _gen()
+gen = _gen("gen_attn_epochs")
+gen64 = _gen("gen_attn_steps64")
+# (generator, its .inc, the first Q register, Q registers)
+LOOPS = {"hd128": (gen, "tk_attn_epochs.inc", gen.Q, 32), "hd64": (gen64, gen64.INC, gen64.Q, 16)}
 
 
-def test_committed_inc_is_the_generator_output():
-    assert (CSRC / "tk_attn_epochs.inc").read_text() == gen.render()
+@pytest.mark.parametrize("loop", LOOPS)
+def test_committed_inc_is_the_generator_output(loop):
+    g, inc, _, _ = LOOPS[loop]
+    assert (CSRC / inc).read_text() == g.render()
 
 
-def test_kernel_clobber_list_matches_the_generator():
+@pytest.mark.parametrize("loop", LOOPS)
+def test_kernel_clobber_list_matches_the_generator(loop):
+    g, inc, _, _ = LOOPS[loop]
     src = (CSRC / "tk_attention.hip").read_text()
-    i = src.index('#include "tk_attn_epochs.inc"')
+    i = src.index(f'#include "{inc}"')
     stmt = src[i:src.index(");", i)]
     clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
-    assert clobbers == gen.CLOBBERED
+    assert clobbers == g.CLOBBERED
     for extra in ('"vcc"', '"scc"', '"memory"'):
         assert extra in stmt
 
@@ -169,8 +177,9 @@ def _asm_lines(program: list[str]) -> list[str]:
     return [l.replace("%=", "0") for l in program]
 
 
-def test_generated_loop_meets_the_wait_states():
-    bad = hazard_violations(_asm_lines(gen.program()))
+@pytest.mark.parametrize("loop", LOOPS)
+def test_generated_loop_meets_the_wait_states(loop):
+    bad = hazard_violations(_asm_lines(LOOPS[loop][0].program()))
     assert not bad, "\n".join(bad[:10])
 
 
@@ -200,17 +209,19 @@ def test_wait_state_checker_finds_planted_mistakes(planted):
     assert hazard_violations(prog), planted
 
 
-def test_loop_registers_stay_in_its_operands_and_clobbers():
-    allowed = {f"v{r}" for r in gen.PINNED | set(gen.CLOBBERED)}
-    q_regs = {f"v{r}" for r in range(gen.Q, gen.Q + 32)}
-    ins, _ = _cfg(_asm_lines(gen.program()))
+@pytest.mark.parametrize("loop", LOOPS)
+def test_loop_registers_stay_in_its_operands_and_clobbers(loop):
+    g, _, q0, nq = LOOPS[loop]
+    allowed = {f"v{r}" for r in g.PINNED | set(g.CLOBBERED)}
+    q_regs = {f"v{r}" for r in range(q0, q0 + nq)}
+    ins, _ = _cfg(_asm_lines(g.program()))
     used = set()
     for x in ins:
         used |= {r for r in x.reads | x.writes if re.fullmatch(r"v\d+", r)}
         assert not (x.writes & q_regs), x.text  # Q is an input-only operand
     assert used <= allowed, sorted(used - allowed)
-    # the pinned P region A and O are both read and written; every clobber is used
-    assert {f"v{r}" for r in gen.CLOBBERED} <= used
+    # every clobber is used
+    assert {f"v{r}" for r in g.CLOBBERED} <= used
 
 
 def test_loop_covers_four_epochs_of_32_mfmas():
@@ -218,3 +229,15 @@ def test_loop_covers_four_epochs_of_32_mfmas():
     assert sum(1 for l in prog if l.startswith("v_mfma")) == 4 * 32
     assert sum(1 for l in prog if l == "s_barrier") == 4
     assert sum(1 for l in prog if l.startswith("global_load_lds")) == 4 * 4
+
+
+def test_hd64_loop_covers_two_steps_of_16_mfmas():
+    prog = gen64.program()
+    assert sum(1 for l in prog if l.startswith("v_mfma")) == 2 * 16
+    assert sum(1 for l in prog if l == "s_barrier") == 2
+    assert sum(1 for l in prog if l.startswith("global_load_lds")) == 2 * 4
+    # 32 exponentials and 16 packs per step, every row-sum term in order
+    temps = tuple(f"v_exp_f32 v{r}," for r in (gen64.T0, gen64.T1, gen64.T2, gen64.T3))
+    assert sum(1 for l in prog if l.startswith(temps)) == 2 * 32
+    dots = [l for l in prog if l.startswith("v_dot2c")]
+    assert len(dots) == 32

@@ -325,15 +325,17 @@ def test_flash_attention_long_ragged(s, hd):
         assert bad == 0, (causal, err)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
 @pytest.mark.parametrize("s", [1024, 1300, 2100])
-def test_flash_attention_epoch_loop_is_bit_identical(s):
-    """head_dim 128, causal: the key tiles below a 256-row query block's diagonal
-    run from the generated asm loop (tk_attn_epochs.inc) when the K/V copy span
-    fits 32-bit offsets.  K/V rows 4 MiB apart put the span past 2^31 bytes for
-    every query block that would use the loop, so the same values take the
-    compiled epochs; the loop changes the instruction order, not the arithmetic,
-    so the two outputs must agree bit for bit (and both with the reference)."""
-    b, h, hd = 1, 1, 128
+def test_flash_attention_epoch_loop_is_bit_identical(s, hd):
+    """Causal, head_dim 128 (256-row query blocks) and 64 (128-row blocks): the
+    key tiles below a query block's diagonal run from a generated asm loop
+    (tk_attn_epochs.inc, tk_attn_steps64.inc) when the K/V copy span fits 32-bit
+    offsets.  K/V rows 4 MiB apart put the span past 2^31 bytes for every query
+    block that would use the loop, so the same values take the compiled steps;
+    the loop changes the instruction order, not the arithmetic, so the two
+    outputs must agree bit for bit (and both with the reference)."""
+    b, h = 1, 1
     q, k, v = _qkv((b, h, s, hd), seed=s)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     compact = ops.flash_attention(qd, kd, vd, hd ** -0.5, True)

@@ -1,0 +1,239 @@
+"""Emit tk_attn_steps64.inc: the hand-ordered steady-state steps of the head_dim-64 causal
+attention (flash_dma_body in tk_attention.hip, 4 waves, 128 query rows per workgroup).
+
+    python gen_attn_steps64.py [directory]    # default: beside this file
+
+The build runs this before compiling tk_attention.hip.
+
+What a step computes
+--------------------
+Step kt of the DMA body (key tile kt = keys 64kt .. 64kt+63), for every wave:
+
+  max       m_tile = scale*log2(e) * (row max of S(kt) over the lane pair, found during the
+            previous step); lazy rescale when any lane's m_tile exceeds m_run + 8:
+            m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new), l_run *= alpha
+  16 slots  slot m < 8: S^T(kt+1) MFMA m (key block m / 4, k-step m % 4);
+            slot m >= 8: O^T += V^T(kt-1) . P^T(kt-1), MFMA m - 8 (head-dim block (m-8) % 2,
+            P block (m-8) / 2); exponential pair m of S(kt) (entries 2m, 2m+1) between the
+            MFMAs -> P(kt), fp16 row sum with v_dot2c; row max of S(kt+1) once its MFMAs are done
+  copies    K tile kt+2 after slot 0, V tile kt+1 after slot 2 (LDS DMA)
+  end       l_run += row sum; O *= alpha when the rescale ran; wait for this step's copies;
+            barrier
+
+Each lane performs the compiled step's operations on the same operands in the same order (the
+MFMA accumulation chains, the exponentials, the fp16 packing and the row-sum order; the row max
+is exact in any order), so the results are bit-identical to it.  The loop runs steps
+[1, 1 + 2*groups), which the host side chooses so that no key tile in them needs a mask and
+every copy is a whole tile; m_run is finite there.  Two steps per iteration: the score, P and
+max registers swap roles between them (the compiled loop's s_a/s_b, pf_a/pf_b, mx_a/mx_b), the
+K slot (2 slots) follows the parity and the V slots (3) rotate through SGPR trackers.
+
+Register map (VGPRs; the asm statement pins or clobbers every one of them)
+--------------------------------------------------------------------------
+  v[64:95]    O^T accumulators, 2 x 16                     (in/out)
+  v[96:111]   Q fragments, 4 x 4                            (in)
+  v[112:143]  scores X: S(kt) at entry and exit             (in/out)
+  v[144:159]  P tile W: P(kt-1) at entry and exit           (in/out)
+  v160        row max of X's scores                         (in/out)
+  v161, v162  m_run, l_run                                  (in/out)
+  v163        row max of Y's scores                         (clobbered)
+  v[164:195]  scores Y                                      (clobbered)
+  v[196:211]  P tile Z                                      (clobbered)
+  v212..v217  temporaries                                   (clobbered)
+  v[218:229]  operand ring, 3 x 4 (K or V fragments)         (clobbered)
+
+Wait states: as in gen_attn_epochs.py (M0 -> LDS DMA 1, MFMA -> VALU 24 or an MFMA-free
+stretch of at least 18 instructions, VALU -> v_permlane32_swap 2, VCC -> s_cbranch_vccz 4,
+v_exp -> VALU 1, v_dot2c -> other VALU 3).
+"""
+from __future__ import annotations
+
+import pathlib
+import sys
+
+O = 64
+Q = 96
+X, W, MXX = 112, 144, 160
+MR, LR = 161, 162
+MXY, Y, Z = 163, 164, 196
+T0, T1, T2, T3 = 212, 213, 214, 215   # exponential pipeline, two pairs
+MX, TMP = T0, T1                      # the max phase ends before the pipeline starts
+ALPHA, LS = 216, 217
+RING = 218                            # 64-bit aligned tuples
+TILE = 8192                           # bytes per K or V tile (64 rows x 128 bytes)
+KSLOTS, VSLOTS = 2, 3
+
+PINNED = set(range(64, 160)) | {MXX, MR, LR}
+CLOBBERED = sorted({MXY} | set(range(164, 230)))
+
+
+def v(a: int, n: int = 1) -> str:
+    return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
+
+
+def step(par: int) -> list[str]:
+    """One step; par 0: scores X current, Y next, P W previous, Z new; par 1 swaps them.
+    Step kt has par = (kt + 1) % 2 (the loop starts at kt = 1)."""
+    s_cur, s_nxt = (X, Y) if par == 0 else (Y, X)
+    p_prev, p_cur = (W, Z) if par == 0 else (Z, W)
+    mx_cur, mx_nxt = (MXX, MXY) if par == 0 else (MXY, MXX)
+    k_rd = par * TILE                     # K(kt+1) is read from slot (kt + 1) % 2 = par
+    k_wr = (1 - par) * TILE               # K(kt+2) is written into slot kt % 2
+
+    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    # ---- row max of S(kt) over the lane pair, lazy rescale ----
+    L += [f"v_mov_b32 {v(TMP)}, {v(mx_cur)}", f"v_mov_b32 {v(MX)}, {v(mx_cur)}", "s_nop 1",
+          f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
+          f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
+          f"v_mul_f32 {v(MX)}, {v(MX)}, %[cs]",                  # m_tile
+          f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",             # m_run + 8
+          f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
+          f"s_cbranch_vccz L_norescale_{par}_%="]
+    L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",                # m_new
+          f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
+          f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
+          f"v_mov_b32 {v(MR)}, {v(TMP)}", "s_nop 0",
+          f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
+          "s_mov_b32 %[flag], 1"]
+    L += [f"L_norescale_{par}_%=:"]
+    # ---- fragment reads: slot m's fragment into ring entry m % 3; read addresses go
+    # through the exponential pair that is idle where the read is issued (ka) ----
+    def reads(m: int, ka: int = -1) -> list[str]:
+        r = RING + 4 * (m % 3)
+        if m < 8:
+            kb2, kk = m // 4, m % 4
+            off = k_rd + kb2 * 4096
+            if kk == 0:
+                return [f"ds_read_b128 {v(r, 4)}, %[kl0] offset:{off}"]
+            return [f"v_xor_b32 {v(ka)}, {kk << 5}, %[kl0]", f"ds_read_b128 {v(r, 4)}, {v(ka)} offset:{off}"]
+        c = m - 8
+        t, d = c // 2, c % 2
+        return [f"v_add_u32 {v(ka)}, %[vrd], %[vl{d}]",
+                f"ds_read_b64_tr_b16 {v(r, 2)}, {v(ka)} offset:{t * 2048}",
+                f"ds_read_b64_tr_b16 {v(r + 2, 2)}, {v(ka)} offset:{t * 2048 + 1024}"]
+
+    def n_ds(m: int) -> int:
+        return 1 if m < 8 else 2
+
+    # ---- exponential pipeline over the slots (pair j: entries 2j, 2j+1 of S(kt)) ----
+    tp = ((T0, T1), (T2, T3))
+
+    def sr(i: int) -> int:
+        return s_cur + i
+
+    def scale(j: int) -> list[str]:
+        a, b = tp[j % 2]
+        return [f"v_fma_f32 {v(a)}, {v(sr(2 * j))}, %[cs], -{v(MR)}",
+                f"v_fma_f32 {v(b)}, {v(sr(2 * j + 1))}, %[cs], -{v(MR)}"]
+
+    def expo(j: int) -> list[str]:
+        a, b = tp[j % 2]
+        return [f"v_exp_f32 {v(a)}, {v(a)}", f"v_exp_f32 {v(b)}, {v(b)}"]
+
+    def pack(j: int) -> list[str]:
+        a, b = tp[j % 2]
+        return [f"v_cvt_pk_f16_f32 {v(p_cur + j)}, {v(a)}, {v(b)}",
+                f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(p_cur + j)}"]
+
+    # ---- row max of S(kt+1): block 0 (MFMAs 0..3) in slots 9..11, block 1 (4..7) in 13..15 ----
+    def nmax(m: int) -> list[str]:
+        plan = {9: (0, 6), 10: (6, 12), 11: (12, 16), 13: (16, 22), 14: (22, 28), 15: (28, 32)}
+        if m not in plan:
+            return []
+        lo, hi = plan[m]
+        if lo == 0:  # first: max3(s0, s1, s2), then pairs from 3 on
+            out = [f"v_max3_f32 {v(mx_nxt)}, {v(s_nxt)}, {v(s_nxt + 1)}, {v(s_nxt + 2)}"]
+            k = 3
+        else:
+            out, k = [], lo
+        while k + 1 < hi:
+            out.append(f"v_max3_f32 {v(mx_nxt)}, {v(mx_nxt)}, {v(s_nxt + k)}, {v(s_nxt + k + 1)}")
+            k += 2
+        if k < hi:
+            out.append(f"v_max_f32 {v(mx_nxt)}, {v(mx_nxt)}, {v(s_nxt + k)}")
+        return out
+
+    # ---- copies ----
+    kcopy = ["s_add_u32 m0, %[ldsw], " + str(k_wr), "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
+             "s_add_u32 m0, m0, 4096", "s_nop 0", "global_load_lds_dwordx4 %[ko1], %[kb]",
+             "v_add_u32 %[ko0], %[kt2], %[ko0]", "v_add_u32 %[ko1], %[kt2], %[ko1]"]
+    vcopy = ["s_add_u32 m0, %[ldsw], %[vwr]", f"s_add_u32 m0, m0, {KSLOTS * TILE}", "s_nop 0",
+             "global_load_lds_dwordx4 %[vo0], %[vb]",
+             "s_add_u32 m0, m0, 4096", "s_nop 0", "global_load_lds_dwordx4 %[vo1], %[vb]",
+             "v_add_u32 %[vo0], %[vt2], %[vo0]", "v_add_u32 %[vo1], %[vt2], %[vo1]"]
+
+    # ---- the 16 slots ----
+    RA = 2
+    for m in range(RA):
+        L += reads(m, tp[1][0])    # pair 1 is free until scale(1) in slot 0
+    L += scale(0)
+    for m in range(16):
+        if m + RA < 16:
+            L += reads(m + RA, tp[(m + 1) % 2][0])  # pack(m-1) has read it, scale(m+1) comes later
+        pending = sum(n_ds(k) for k in range(m + 1, min(16, m + RA + 1)))
+        L.append(f"s_waitcnt lgkmcnt({pending})")
+        r = RING + 4 * (m % 3)
+        if m < 8:
+            kb2, kk = m // 4, m % 4
+            src_c = "0" if kk == 0 else v(s_nxt + 16 * kb2, 16)
+            L.append(f"v_mfma_f32_32x32x16_f16 {v(s_nxt + 16 * kb2, 16)}, {v(r, 4)}, {v(Q + 4 * kk, 4)}, {src_c}")
+        else:
+            c = m - 8
+            t, d = c // 2, c % 2
+            L.append(f"v_mfma_f32_32x32x16_f16 {v(O + 16 * d, 16)}, {v(r, 4)}, {v(p_prev + 4 * t, 4)}, "
+                     f"{v(O + 16 * d, 16)}")
+        L += expo(m)
+        L += scale(m + 1) if m + 1 < 16 else ["s_nop 1"]
+        L += pack(m)
+        L += nmax(m)
+        if m == 0:
+            L += kcopy
+        if m == 2:
+            L += vcopy
+    L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
+    # ---- O rescale ----
+    L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{par}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
+    L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(32)]
+    L += [f"L_noscale_{par}_%=:"]
+    # ---- end: this step's copies have landed; barrier; next V slots ----
+    L += ["s_waitcnt vmcnt(0) lgkmcnt(0)", "s_barrier",
+          f"s_add_u32 %[vrd], %[vrd], {TILE}", f"s_cmp_eq_u32 %[vrd], {VSLOTS * TILE}",
+          "s_cselect_b32 %[vrd], 0, %[vrd]",
+          f"s_add_u32 %[vwr], %[vwr], {TILE}", f"s_cmp_eq_u32 %[vwr], {VSLOTS * TILE}",
+          "s_cselect_b32 %[vwr], 0, %[vwr]"]
+    return L
+
+
+def program() -> list[str]:
+    """M0 saved, `groups` iterations of two steps, M0 restored."""
+    # the scores and P tile handed in were written by MFMAs and VALU ops of the compiled code
+    L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    L += ["L_steps_%=:"]
+    L += step(0) + step(1)
+    L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_steps_%="]
+    # the compiled code after the statement reads O and the scores: MFMA result latency first
+    L += ["s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    return L
+
+
+INC = "tk_attn_steps64.inc"
+
+
+def render() -> str:
+    head = "// Generated by gen_attn_steps64.py; do not edit.\n"
+    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program())
+    return head + body + "\n"
+
+
+def write(directory: pathlib.Path | None = None) -> pathlib.Path:
+    path = (directory or pathlib.Path(__file__).resolve().parent) / INC
+    text = render()
+    if not path.exists() or path.read_text() != text:
+        path.write_text(text)
+    return path
+
+
+if __name__ == "__main__":
+    out = write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None)
+    prog = program()
+    print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")

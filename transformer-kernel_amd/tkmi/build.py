@@ -5,8 +5,8 @@
 
 Every ``csrc/*.hip`` file is compiled to an object under
 ``transformer-kernel_amd/_build/`` (in parallel), then linked into
-``transformer-kernel_amd/tkmi/libtkmi.so``; ``csrc/gen_attn_epochs.py`` first
-rewrites the generated ``csrc/tk_attn_epochs.inc``.  The flags target gfx950 only.
+``transformer-kernel_amd/tkmi/libtkmi.so``; ``csrc/gen_attn_epochs.py`` and
+``csrc/gen_attn_steps64.py`` first rewrite the generated ``csrc/tk_attn_*.inc``.  The flags target gfx950 only.
 ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the compiler from
 emitting packed-fp32 VALU instructions (the host pass warns that it does not
 know the feature; that is harmless).
@@ -85,13 +85,14 @@ def _compile(src: pathlib.Path):
 
 
 def generate() -> None:
-    """Write the generated kernel sources (the attention steady-state asm loop)."""
+    """Write the generated kernel sources (the attention steady-state asm loops)."""
     import importlib.util
 
-    spec = importlib.util.spec_from_file_location("gen_attn_epochs", CSRC / "gen_attn_epochs.py")
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
-    mod.write()
+    for name in ("gen_attn_epochs", "gen_attn_steps64"):
+        spec = importlib.util.spec_from_file_location(name, CSRC / f"{name}.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.write()
 
 
 def build(verbose: bool = True, jobs: int = 0) -> pathlib.Path:
