@@ -353,6 +353,20 @@ def test_flash_attention_epoch_loop_is_bit_identical(s, hd):
     assert bad == 0, err
 
 
+@pytest.mark.parametrize("hd,s", [(64, n) for n in (319, 320, 383, 384, 385, 447, 448, 449, 575, 576, 640)]
+                         + [(128, n) for n in (575, 576, 639, 640, 641, 767, 768, 769, 832, 1023, 1025)])
+def test_flash_attention_epoch_loop_boundaries(hd, s):
+    """Causal lengths around the points where the asm steady state's step count
+    changes (head_dim 64: 128-row query blocks, steps up to min(q0/64 - 1,
+    min(n_kt, S/64) - 3); head_dim 128: 256-row blocks, epochs up to
+    min(q0/64, min(n_kt, S/64) - 2)), against the reference."""
+    b, h = 1, 2
+    q, k, v = _qkv((b, h, s, hd), seed=3 * s + hd)
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, True)
+    bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, True))
+    assert bad == 0, err
+
+
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
 def test_flash_attention_v_rows_8_byte_aligned(causal):
     """head_dim 128 with V rows only 8-byte aligned: the non-causal body loads V
