@@ -31,8 +31,22 @@ def _gen(name):
 
 gen = _gen("gen_attn_epochs")
 gen64 = _gen("gen_attn_steps64")
+class _W8:
+    """The 8-wave head_dim-64 loop through the common generator interface."""
+    CLOBBERED, PINNED = gen64.CLOBBERED, gen64.PINNED
+
+    @staticmethod
+    def program():
+        return gen64.program(8)
+
+    @staticmethod
+    def render():
+        return gen64.render(8)
+
+
 # (generator, its .inc, the first Q register, Q registers)
-LOOPS = {"hd128": (gen, "tk_attn_epochs.inc", gen.Q, 32), "hd64": (gen64, gen64.INC, gen64.Q, 16)}
+LOOPS = {"hd128": (gen, "tk_attn_epochs.inc", gen.Q, 32), "hd64": (gen64, gen64.INCS[4], gen64.Q, 16),
+         "hd64w8": (_W8, gen64.INCS[8], gen64.Q, 16)}
 
 
 @pytest.mark.parametrize("loop", LOOPS)
@@ -47,6 +61,9 @@ def test_kernel_clobber_list_matches_the_generator(loop):
     src = (CSRC / "tk_attention.hip").read_text()
     i = src.index(f'#include "{inc}"')
     stmt = src[i:src.index(");", i)]
+    if "OPERANDS" in stmt:  # the operand list is a macro defined just before the statement
+        d = src.rindex("#define TK_", 0, i)
+        stmt = src[d:i]
     clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
     assert clobbers == g.CLOBBERED
     for extra in ('"vcc"', '"scc"', '"memory"'):
@@ -241,3 +258,12 @@ def test_hd64_loop_covers_two_steps_of_16_mfmas():
     assert sum(1 for l in prog if l.startswith(temps)) == 2 * 32
     dots = [l for l in prog if l.startswith("v_dot2c")]
     assert len(dots) == 32
+
+
+def test_hd64_loops_differ_only_in_the_copies():
+    four, eight = gen64.program(4), gen64.program(8)
+    strip = lambda prog: [l for l in prog if not l.startswith(("global_load_lds", "s_add_u32 m0, m0"))
+                          and "%[ko1]" not in l and "%[vo1]" not in l and l != "s_nop 0"]
+    assert strip(four) == strip(eight)
+    assert sum(1 for l in four if l.startswith("global_load_lds")) == 2 * sum(
+        1 for l in eight if l.startswith("global_load_lds"))

@@ -244,10 +244,10 @@ def test_hot_kernels_use_no_scratch():
     missing = [k for k in hot if k not in usage]
     assert not missing, missing
     spilled = {k: usage[k]["scratch"] for k in hot if usage[k].get("scratch", 0) > 0}
-    # The head_dim-64 causal kernel with the hand-ordered loop keeps three
-    # lane-derived addresses in scratch across the loop: stored once before it
-    # and reloaded once after it, outside every loop of the kernel.
-    allowed = {f"_ZN2tk12_GLOBAL__N_116flash_fwd_kernelILi64ELi4ELb1ELb0EEEvNS0_8AttnArgsE": 12}
+    # The head_dim-64 causal kernels with the hand-ordered loop (4 and 8 waves)
+    # keep three lane-derived addresses in scratch across the loop: stored once
+    # before it and reloaded once after it, outside every loop of the kernel.
+    allowed = {f"_ZN2tk12_GLOBAL__N_116flash_fwd_kernelILi64ELi{nw}ELb1ELb0EEEvNS0_8AttnArgsE": 12 for nw in (4, 8)}
     spilled = {k: b for k, b in spilled.items() if b > allowed.get(k, 0)}
     assert not spilled, spilled
 

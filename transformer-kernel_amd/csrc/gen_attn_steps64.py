@@ -1,5 +1,6 @@
-"""Emit tk_attn_steps64.inc: the hand-ordered steady-state steps of the head_dim-64 causal
-attention (flash_dma_body in tk_attention.hip, 4 waves, 128 query rows per workgroup).
+"""Emit tk_attn_steps64{,_w8}.inc: the hand-ordered steady-state steps of the head_dim-64 causal
+attention (flash_dma_body in tk_attention.hip; 4 waves and 128 query rows per workgroup up to
+32768 keys, 8 waves and 256 rows beyond -- the two differ only in the copies per wave).
 
     python gen_attn_steps64.py [directory]    # default: beside this file
 
@@ -71,8 +72,9 @@ def v(a: int, n: int = 1) -> str:
     return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
 
 
-def step(par: int) -> list[str]:
-    """One step; par 0: scores X current, Y next, P W previous, Z new; par 1 swaps them.
+def step(par: int, nw: int = 4) -> list[str]:
+    """One step of an nw-wave workgroup (4: two 1 KB copies per tile and wave, 8: one);
+    par 0: scores X current, Y next, P W previous, Z new; par 1 swaps them.
     Step kt has par = (kt + 1) % 2 (the loop starts at kt = 1)."""
     s_cur, s_nxt = (X, Y) if par == 0 else (Y, X)
     p_prev, p_cur = (W, Z) if par == 0 else (Z, W)
@@ -154,13 +156,16 @@ def step(par: int) -> list[str]:
         return out
 
     # ---- copies ----
-    kcopy = ["s_add_u32 m0, %[ldsw], " + str(k_wr), "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
-             "s_add_u32 m0, m0, 4096", "s_nop 0", "global_load_lds_dwordx4 %[ko1], %[kb]",
-             "v_add_u32 %[ko0], %[kt2], %[ko0]", "v_add_u32 %[ko1], %[kt2], %[ko1]"]
+    # copy i of wave w fills LDS bytes (w + i*nw) * 1024 of the slot
+    cpw = (TILE // 1024) // nw
+    kcopy = ["s_add_u32 m0, %[ldsw], " + str(k_wr), "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]"]
     vcopy = ["s_add_u32 m0, %[ldsw], %[vwr]", f"s_add_u32 m0, m0, {KSLOTS * TILE}", "s_nop 0",
-             "global_load_lds_dwordx4 %[vo0], %[vb]",
-             "s_add_u32 m0, m0, 4096", "s_nop 0", "global_load_lds_dwordx4 %[vo1], %[vb]",
-             "v_add_u32 %[vo0], %[vt2], %[vo0]", "v_add_u32 %[vo1], %[vt2], %[vo1]"]
+             "global_load_lds_dwordx4 %[vo0], %[vb]"]
+    for i in range(1, cpw):
+        kcopy += [f"s_add_u32 m0, m0, {nw * 1024}", "s_nop 0", f"global_load_lds_dwordx4 %[ko{i}], %[kb]"]
+        vcopy += [f"s_add_u32 m0, m0, {nw * 1024}", "s_nop 0", f"global_load_lds_dwordx4 %[vo{i}], %[vb]"]
+    kcopy += [f"v_add_u32 %[ko{i}], %[kt2], %[ko{i}]" for i in range(cpw)]
+    vcopy += [f"v_add_u32 %[vo{i}], %[vt2], %[vo{i}]" for i in range(cpw)]
 
     # ---- the 16 slots ----
     RA = 2
@@ -204,36 +209,40 @@ def step(par: int) -> list[str]:
     return L
 
 
-def program() -> list[str]:
+def program(nw: int = 4) -> list[str]:
     """M0 saved, `groups` iterations of two steps, M0 restored."""
     # the scores and P tile handed in were written by MFMAs and VALU ops of the compiled code
     L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]", "s_nop 7", "s_nop 7", "s_nop 7"]
     L += ["L_steps_%=:"]
-    L += step(0) + step(1)
+    L += step(0, nw) + step(1, nw)
     L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_steps_%="]
     # the compiled code after the statement reads O and the scores: MFMA result latency first
     L += ["s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
     return L
 
 
-INC = "tk_attn_steps64.inc"
+INCS = {4: "tk_attn_steps64.inc", 8: "tk_attn_steps64_w8.inc"}
+INC = INCS[4]
 
 
-def render() -> str:
-    head = "// Generated by gen_attn_steps64.py; do not edit.\n"
-    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program())
+def render(nw: int = 4) -> str:
+    head = f"// Generated by gen_attn_steps64.py ({nw} waves); do not edit.\n"
+    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program(nw))
     return head + body + "\n"
 
 
-def write(directory: pathlib.Path | None = None) -> pathlib.Path:
-    path = (directory or pathlib.Path(__file__).resolve().parent) / INC
-    text = render()
-    if not path.exists() or path.read_text() != text:
-        path.write_text(text)
-    return path
+def write(directory: pathlib.Path | None = None) -> list[pathlib.Path]:
+    paths = []
+    for nw, name in INCS.items():
+        path = (directory or pathlib.Path(__file__).resolve().parent) / name
+        text = render(nw)
+        if not path.exists() or path.read_text() != text:
+            path.write_text(text)
+        paths.append(path)
+    return paths
 
 
 if __name__ == "__main__":
-    out = write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None)
-    prog = program()
-    print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")
+    for out, nw in zip(write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None), INCS):
+        prog = program(nw)
+        print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")
