@@ -44,9 +44,22 @@ class _W8:
         return gen64.render(8)
 
 
+class _KMask:
+    """The key-masked head_dim-128 loop through the common generator interface."""
+    CLOBBERED, PINNED = gen.CLOBBERED, gen.PINNED
+
+    @staticmethod
+    def program():
+        return gen.program(True)
+
+    @staticmethod
+    def render():
+        return gen.render(True)
+
+
 # (generator, its .inc, the first Q register, Q registers)
-LOOPS = {"hd128": (gen, "tk_attn_epochs.inc", gen.Q, 32), "hd64": (gen64, gen64.INCS[4], gen64.Q, 16),
-         "hd64w8": (_W8, gen64.INCS[8], gen64.Q, 16)}
+LOOPS = {"hd128": (gen, gen.INCS[False], gen.Q, 32), "hd128kmask": (_KMask, gen.INCS[True], gen.Q, 32),
+         "hd64": (gen64, gen64.INCS[4], gen64.Q, 16), "hd64w8": (_W8, gen64.INCS[8], gen64.Q, 16)}
 
 
 @pytest.mark.parametrize("loop", LOOPS)
@@ -64,6 +77,9 @@ def test_kernel_clobber_list_matches_the_generator(loop):
     if "OPERANDS" in stmt:  # the operand list is a macro defined just before the statement
         d = src.rindex("#define TK_", 0, i)
         stmt = src[d:i]
+    elif "_CLOBS" in stmt:  # outputs, inputs and clobbers are macros defined before the statements
+        d = src.rindex("#define TK_EPOCH_CLOBS", 0, i)
+        stmt = src[d:src.index("\n    if constexpr", d)] + stmt
     clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
     assert clobbers == g.CLOBBERED
     for extra in ('"vcc"', '"scc"', '"memory"'):
@@ -267,3 +283,20 @@ def test_hd64_loops_differ_only_in_the_copies():
     assert strip(four) == strip(eight)
     assert sum(1 for l in four if l.startswith("global_load_lds")) == 2 * sum(
         1 for l in eight if l.startswith("global_load_lds"))
+
+
+def test_key_masked_loop_adds_only_the_mask_work():
+    """The key-masked loop is the dense one plus, per epoch, the validity-byte load,
+    the key bits, 32 score selects and the m = -inf guard."""
+    dense, masked = gen.program(False), gen.program(True)
+    extra = [l for l in masked if l not in dense]
+    assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "s_waitcnt vmcnt(4)", "v_cmp_",
+                             "s_mov_b32 s9", "s_mov_b64 s[94:95]", "s_bfe_i32", "v_cndmask_b32",
+                             "v_mov_b32 v196, 0xff800000")) for l in extra), extra[:5]
+    assert sum(1 for l in masked if l.startswith("v_cndmask_b32")) == 4 * (32 + 2)
+    it = iter(masked)  # the dense loop is a subsequence of the masked one, in order
+    assert all(any(m == l for m in it) for l in dense)
+    src = (CSRC / "tk_attention.hip").read_text()
+    i = src.index(f'#include "{gen.INCS[True]}"')
+    clobs = src[i:src.index(");", i)]
+    assert all(f'"s{r}"' in clobs for r in gen.S_CLOBBERED)

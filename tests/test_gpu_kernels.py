@@ -420,7 +420,8 @@ def _attention_ref_keymask(q, k, v, scale, causal, key_valid):
     return torch.matmul(probs, v.float()).transpose(1, 2).reshape(b, s, h * hd)
 
 
-@pytest.mark.parametrize("shape", [(2, 4, 128, 32), (3, 2, 100, 64), (2, 2, 700, 128), (1, 2, 64, 16),
+@pytest.mark.parametrize("shape", [(2, 4, 128, 32), (3, 2, 100, 64), (2, 2, 700, 128), (1, 2, 1300, 128),
+                                   (1, 2, 64, 16),
                                    (1, 2, 300, 256), (2, 1, 64, 256),  # head_dim 256 (generic vector kernel)
                                    (2, 2, 90, 48)],                    # element-load kernel
                          ids=lambda s: "b{}h{}s{}d{}".format(*s))
@@ -440,6 +441,44 @@ def test_flash_attention_key_mask(shape, causal):
     bad, err = or_rule_violations(out[seen], ref[seen])
     assert bad == 0, err
     assert not bool(torch.isfinite(out[~seen]).all()) or not bool((~seen).any())
+
+
+@pytest.mark.parametrize("pattern", ["tail", "head", "holes"])
+def test_flash_attention_key_masked_loop_is_bit_identical(pattern):
+    """head_dim 128, causal, with a key mask: the generated key-masked loop
+    (tk_attn_epochs_kmask.inc) against the compiled epochs, forced as in
+    test_flash_attention_epoch_loop_is_bit_identical by K/V rows 4 MiB apart.
+    tail: padded keys at the end; head: the first 200 keys invalid, so query
+    blocks enter the loop with rows that have seen no valid key (m = -inf);
+    holes: about 30 % of keys invalid.  Rows with no valid key come out
+    non-finite on both paths."""
+    b, h, s, hd = 2, 1, 1300, 128
+    q, k, v = _qkv((b, h, s, hd), seed=97)
+    kv = torch.ones(b, s, dtype=torch.bool)
+    if pattern == "tail":
+        kv[0, 1000:] = False
+        kv[1, 700:] = False
+    elif pattern == "head":
+        kv[:, :200] = False
+    else:
+        kv = torch.rand(b, s, generator=torch.Generator().manual_seed(5)) > 0.3
+    qd, kd, vd, kvd = q.to(DEV), k.to(DEV), v.to(DEV), kv.to(DEV)
+    compact = ops.flash_attention(qd, kd, vd, hd ** -0.5, True, key_valid=kvd)
+    rs = 1 << 21
+    wide_k = torch.zeros(b, s, rs, dtype=torch.float16, device=DEV)
+    wide_v = torch.zeros(b, s, rs, dtype=torch.float16, device=DEV)
+    wide_k[:, :, :hd] = kd[:, 0]
+    wide_v[:, :, :hd] = vd[:, 0]
+    kw, vw = wide_k[:, :, :hd][:, None], wide_v[:, :, :hd][:, None]
+    assert kw.stride(2) == rs and torch.equal(kw, kd)
+    spread = ops.flash_attention(qd, kw, vw, hd ** -0.5, True, key_valid=kvd)
+    del wide_k, wide_v
+    same = (compact == spread) | (torch.isnan(compact) & torch.isnan(spread))
+    assert bool(same.all())
+    ref = _attention_ref_keymask(q, k, v, hd ** -0.5, True, kv)
+    seen = (kv[:, None, :] & torch.ones(s, s, dtype=torch.bool).tril()[None]).any(-1)
+    bad, err = or_rule_violations(compact.cpu()[seen], ref[seen])
+    assert bad == 0, err
 
 
 def test_attention_support_probes():

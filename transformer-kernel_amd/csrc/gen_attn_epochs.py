@@ -82,8 +82,38 @@ def v(a: int, n: int = 1) -> str:
     return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
 
 
-def epoch(u: int) -> list[str]:
-    """Instructions of the epoch at loop position u (0..3)."""
+# key-masked variant: physical SGPRs (inline asm cannot name halves of a 64-bit operand)
+S_MASK = (88, 90)     # two lane-mask pairs, alternating
+S_KB = (92, 93)       # key-validity bits of the tile: lanes' keys 0..31, 32..63
+S_NOKEY = 94          # s[94:95]: lanes whose m_run is still -inf (no valid key yet)
+S_CLOBBERED = list(range(88, 96))
+NEG_INF = "0xff800000"
+
+
+def key_mask(sr) -> list[str]:
+    """Scores of keys whose validity byte is 0 -> -inf.  Entry i = 16*kb2 + r of a lane holds
+    key 32*kb2 + 8*(r/4) + r%4 + 4g (g = lane / 32), so its lane mask takes bit j of the tile's
+    bits for lanes 0..31 and bit j+4 for lanes 32..63 (s_bfe_i32 of one bit: 0 or -1)."""
+    def mask(i: int, pair: int) -> list[str]:
+        kb2, r = i >> 4, i & 15
+        j = 32 * kb2 + 8 * (r >> 2) + (r & 3)
+        lo, hi = j, j + 4
+        return [f"s_bfe_i32 s{pair}, s{S_KB[lo >> 5]}, {(lo & 31) | (1 << 16)}",
+                f"s_bfe_i32 s{pair + 1}, s{S_KB[hi >> 5]}, {(hi & 31) | (1 << 16)}"]
+
+    def select(i: int, pair: int) -> list[str]:
+        return [f"v_cndmask_b32 {v(sr(i))}, {v(ALPHA)}, {v(sr(i))}, s[{pair}:{pair + 1}]"]
+
+    out = [f"v_mov_b32 {v(ALPHA)}, {NEG_INF}"] + mask(0, S_MASK[0])
+    for i in range(32):
+        if i + 1 < 32:
+            out += mask(i + 1, S_MASK[(i + 1) % 2])  # two instructions between a mask and its use
+        out += select(i, S_MASK[i % 2])
+    return out
+
+
+def epoch(u: int, kmask: bool = False) -> list[str]:
+    """Instructions of the epoch at loop position u (0..3); kmask: the key-masked variant."""
     pp, pc = (P[0], P[1]) if u % 2 == 0 else (P[1], P[0])
     sb = (pc, SB1)  # scores: key block 0 in the new-P region, key block 1 in SB1
 
@@ -91,6 +121,8 @@ def epoch(u: int) -> list[str]:
         return sb[i >> 4] + (i & 15)
 
     L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    if kmask:  # this tile's key-validity bytes, one per lane, ahead of the copies (vmcnt order)
+        L += [f"global_load_ubyte {v(TX)}, %[koff], %[kvb]", "v_add_u32 %[koff], 64, %[koff]"]
     # ---- copies: K(e+2) into the K slot kwr, V(e+1) into V slot (u + 2) % 4 ----
     L += ["s_add_u32 m0, %[ldsw], %[kwr]", "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
           "s_add_u32 m0, m0, 8192", "s_nop 0", "global_load_lds_dwordx4 %[ko1], %[kb]"]
@@ -125,6 +157,10 @@ def epoch(u: int) -> list[str]:
     # ---- row max over the lane pair, lazy rescale ----
     # two interleaved chains (key blocks 0 and 1), so no max waits on the one before it
     L += ["s_nop 7", "s_nop 7", "s_nop 7"]
+    if kmask:  # the byte load is older than this epoch's four copies
+        L += ["s_waitcnt vmcnt(4)", f"v_cmp_ne_u32 vcc, 0, {v(TX)}",
+              f"s_mov_b32 s{S_KB[0]}, vcc_lo", f"s_mov_b32 s{S_KB[1]}, vcc_hi"]
+        L += key_mask(sr)
     L += [f"v_max3_f32 {v(MX)}, {v(sr(0))}, {v(sr(1))}, {v(sr(2))}",
           f"v_max3_f32 {v(TMP)}, {v(sr(16))}, {v(sr(17))}, {v(sr(18))}"]
     for k in range(3, 15, 2):
@@ -145,6 +181,9 @@ def epoch(u: int) -> list[str]:
           f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
           "s_mov_b32 %[flag], 1"]
     L += [f"L_norescale_{u}_%=:"]
+    if kmask:  # rows with no valid key so far: exponentials against 0, m_run restored after
+        L += [f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(MR)}", f"s_mov_b64 s[{S_NOKEY}:{S_NOKEY + 1}], vcc",
+              f"v_cndmask_b32 {v(MR)}, {v(MR)}, 0, vcc"]
 
     # ---- P.V phase: O^T += V^T(e-1) P^T(e-1); exponentials of S(e) between the MFMAs ----
     vslot = u * TILE
@@ -191,6 +230,9 @@ def epoch(u: int) -> list[str]:
     L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{u}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
     L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(64)]
     L += [f"L_noscale_{u}_%=:"]
+    if kmask:
+        L += [f"v_mov_b32 {v(ALPHA)}, {NEG_INF}",
+              f"v_cndmask_b32 {v(MR)}, {v(MR)}, {v(ALPHA)}, s[{S_NOKEY}:{S_NOKEY + 1}]"]
     # ---- end: this epoch's copies may stay in flight, the previous epoch's have landed ----
     L += ["s_waitcnt vmcnt(4)", "s_barrier",
           "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
@@ -198,22 +240,25 @@ def epoch(u: int) -> list[str]:
     return L
 
 
-def program() -> list[str]:
+def program(kmask: bool = False) -> list[str]:
     """The whole asm body: M0 saved, `groups` iterations of 4 epochs, M0 restored."""
     L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]",
          "s_mov_b32 %[krd], %[krd0]", "s_mov_b32 %[kwr], %[kwr0]", "s_nop 1"]
     L += ["L_epochs_%=:"]
     for u in range(4):
-        L += epoch(u)
+        L += epoch(u, kmask)
     L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_epochs_%="]
     # the compiled code after the statement reads O: MFMA result latency first
     L += ["s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
     return L
 
 
-def render() -> str:
-    head = "// Generated by gen_attn_epochs.py; do not edit.\n"
-    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program())
+INCS = {False: "tk_attn_epochs.inc", True: "tk_attn_epochs_kmask.inc"}
+
+
+def render(kmask: bool = False) -> str:
+    head = "// Generated by gen_attn_epochs.py%s; do not edit.\n" % (" (key-masked)" if kmask else "")
+    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program(kmask))
     return head + body + "\n"
 
 
@@ -221,15 +266,18 @@ def clobber_list() -> str:
     return ", ".join(f'"v{r}"' for r in CLOBBERED)
 
 
-def write(path: pathlib.Path | None = None) -> pathlib.Path:
-    path = path or pathlib.Path(__file__).resolve().parent / "tk_attn_epochs.inc"
-    text = render()
-    if not path.exists() or path.read_text() != text:
-        path.write_text(text)
-    return path
+def write(directory: pathlib.Path | None = None) -> list[pathlib.Path]:
+    paths = []
+    for kmask, name in INCS.items():
+        path = (directory or pathlib.Path(__file__).resolve().parent) / name
+        text = render(kmask)
+        if not path.exists() or path.read_text() != text:
+            path.write_text(text)
+        paths.append(path)
+    return paths
 
 
 if __name__ == "__main__":
-    out = write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None)
-    prog = program()
-    print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")
+    for out, kmask in zip(write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None), INCS):
+        prog = program(kmask)
+        print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")

@@ -1374,19 +1374,23 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
   f16x8 pf_a[4], pf_b[4];
   const bool older = wave < NW / 2;
 
-  // ---- hand-ordered steady state (head_dim 128, 8 waves, causal, no key mask) ----
+  // ---- hand-ordered steady state (head_dim 128, 8 waves, causal; with or without key mask) ----
   // Epochs [1, 1 + 4*groups) run from one asm loop (tk_attn_epochs.inc, made by
   // gen_attn_epochs.py), in one instruction order for every wave.  Each lane does
   // the arithmetic of the compiled epoch in the same order, so O, m and l come out
   // bit-identical; what changes is the schedule (C4 shape b4 h16 s8192: 1239-1253
-  // -> 1137 us in same-box A/B runs).  The epochs it covers need no mask (every
-  // key tile lies below q0, so below every row of the workgroup) and copy only
+  // -> 1137 us in same-box A/B runs).  With a key mask the loop is
+  // tk_attn_epochs_kmask.inc: each epoch also reads its tile's validity bytes,
+  // sets invalid keys' scores to -inf and, like the compiled epoch, exponentiates
+  // against 0 for rows with no valid key yet.  The epochs it covers need no
+  // causal or length mask (every key tile lies below q0, so below every row of
+  // the workgroup) and copy only
   // whole tiles (K tile e+2 <= e_lim+1 < S/kBN), so none of the compiled epoch's
   // clamps and guards apply.  The copies use 32-bit offsets from the K and V
   // bases (span check), and the read addresses are formed by XOR on bits 5-7 of
   // a 256-byte-aligned row offset.
   int groups = 0;
-  if constexpr (HD == 128 && NW == 8 && CAUSAL && !KMASK) {
+  if constexpr (HD == 128 && NW == 8 && CAUSAL) {
     const int e_lim = min(q0 / kBN, min(n_kt, p.S / kBN) - 2);
     const int64_t span =
         ((int64_t)n_kt + 2) * max(k_tile, v_tile) * 2 + (int64_t)kBN * max(p.ks[2], p.vs[2]) * 2;
@@ -1411,25 +1415,44 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
     const float cs = p.scale_log2;
     const uint32_t krd0 = TILE, kwr0 = 0;  // epoch 1 reads K slot 1, writes K(3) into slot 0
     uint32_t msave, cnt, krd, kwr, flag;
-    asm volatile(
+#define TK_EPOCH_OUTS \
+      [o0] "+{v[64:79]}"(acc_o[0]), [o1] "+{v[80:95]}"(acc_o[1]), [o2] "+{v[96:111]}"(acc_o[2]), \
+      [o3] "+{v[112:127]}"(acc_o[3]), [pa0] "+{v[160:163]}"(pf_a[0]), [pa1] "+{v[164:167]}"(pf_a[1]), \
+      [pa2] "+{v[168:171]}"(pf_a[2]), [pa3] "+{v[172:175]}"(pf_a[3]), [mr] "+{v192}"(m_run), \
+      [lr] "+{v193}"(l_run), [ko0] "+&v"(ko[0]), [ko1] "+&v"(ko[1]), [vo0] "+&v"(vo[0]), \
+      [vo1] "+&v"(vo[1]), [msave] "=&s"(msave), [cnt] "=&s"(cnt), [krd] "=&s"(krd), [kwr] "=&s"(kwr), \
+      [flag] "=&s"(flag)
+#define TK_EPOCH_INS \
+      [q0] "{v[128:131]}"(qf[0]), [q1] "{v[132:135]}"(qf[1]), [q2] "{v[136:139]}"(qf[2]), \
+      [q3] "{v[140:143]}"(qf[3]), [q4] "{v[144:147]}"(qf[4]), [q5] "{v[148:151]}"(qf[5]), \
+      [q6] "{v[152:155]}"(qf[6]), [q7] "{v[156:159]}"(qf[7]), [kl0] "v"(kl0), [vl0] "v"(vl[0]), \
+      [vl1] "v"(vl[1]), [vl2] "v"(vl[2]), [vl3] "v"(vl[3]), [kb] "s"(kb), [vb] "s"(vb), \
+      [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), [cs] "s"(cs), [groups] "s"(groups), \
+      [krd0] "s"(krd0), [kwr0] "s"(kwr0)
+#define TK_EPOCH_CLOBS \
+      "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187", \
+      "v188", "v189", "v190", "v191", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", \
+      "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213", \
+      "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225", \
+      "v226", "v227", "vcc", "scc", "memory"
+    if constexpr (KMASK) {
+      // the validity byte of key 64e + lane is read in epoch e, from e = 1
+      uint32_t koff = lane + kBN;
+      asm volatile(
+#include "tk_attn_epochs_kmask.inc"
+          : TK_EPOCH_OUTS, [koff] "+&v"(koff)
+          : TK_EPOCH_INS, [kvb] "s"(kvb)
+          : TK_EPOCH_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+    } else {
+      asm volatile(
 #include "tk_attn_epochs.inc"
-        : [o0] "+{v[64:79]}"(acc_o[0]), [o1] "+{v[80:95]}"(acc_o[1]), [o2] "+{v[96:111]}"(acc_o[2]),
-          [o3] "+{v[112:127]}"(acc_o[3]), [pa0] "+{v[160:163]}"(pf_a[0]), [pa1] "+{v[164:167]}"(pf_a[1]),
-          [pa2] "+{v[168:171]}"(pf_a[2]), [pa3] "+{v[172:175]}"(pf_a[3]), [mr] "+{v192}"(m_run),
-          [lr] "+{v193}"(l_run), [ko0] "+&v"(ko[0]), [ko1] "+&v"(ko[1]), [vo0] "+&v"(vo[0]),
-          [vo1] "+&v"(vo[1]), [msave] "=&s"(msave), [cnt] "=&s"(cnt), [krd] "=&s"(krd), [kwr] "=&s"(kwr),
-          [flag] "=&s"(flag)
-        : [q0] "{v[128:131]}"(qf[0]), [q1] "{v[132:135]}"(qf[1]), [q2] "{v[136:139]}"(qf[2]),
-          [q3] "{v[140:143]}"(qf[3]), [q4] "{v[144:147]}"(qf[4]), [q5] "{v[148:151]}"(qf[5]),
-          [q6] "{v[152:155]}"(qf[6]), [q7] "{v[156:159]}"(qf[7]), [kl0] "v"(kl0), [vl0] "v"(vl[0]),
-          [vl1] "v"(vl[1]), [vl2] "v"(vl[2]), [vl3] "v"(vl[3]), [kb] "s"(kb), [vb] "s"(vb),
-          [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), [cs] "s"(cs), [groups] "s"(groups),
-          [krd0] "s"(krd0), [kwr0] "s"(kwr0)
-        : "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187",
-          "v188", "v189", "v190", "v191", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201",
-          "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213",
-          "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225",
-          "v226", "v227", "vcc", "scc", "memory");
+          : TK_EPOCH_OUTS
+          : TK_EPOCH_INS
+          : TK_EPOCH_CLOBS);
+    }
+#undef TK_EPOCH_OUTS
+#undef TK_EPOCH_INS
+#undef TK_EPOCH_CLOBS
   };
   // After the loop (or in its place) the copy addresses are rebuilt from an
   // opaque lane id rather than kept live across it: held there they spill.
@@ -1456,6 +1479,7 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
     if (groups > 0) {
       run_epochs();
       e += 4 * groups;
+      if constexpr (KMASK) kbits_cur = (uint64_t)__ballot(key_byte(e) != 0);  // the loop keeps its own
     }
     after_epochs();
     for (; e + 1 < n_kt; e += 2) {
@@ -1490,6 +1514,7 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
     if (groups > 0) {
       run_epochs();
       e += 4 * groups;
+      if constexpr (KMASK) kbits_cur = (uint64_t)__ballot(key_byte(e) != 0);  // the loop keeps its own
     }
     after_epochs();
     for (; e + 1 < n_kt; e += 2) {
