@@ -31,17 +31,18 @@ def _gen(name):
 
 gen = _gen("gen_attn_epochs")
 gen64 = _gen("gen_attn_steps64")
-class _W8:
-    """The 8-wave head_dim-64 loop through the common generator interface."""
+class _G64:
+    """A head_dim-64 loop variant through the common generator interface."""
     CLOBBERED, PINNED = gen64.CLOBBERED, gen64.PINNED
 
-    @staticmethod
-    def program():
-        return gen64.program(8)
+    def __init__(self, nw, kmask):
+        self.nw, self.kmask = nw, kmask
 
-    @staticmethod
-    def render():
-        return gen64.render(8)
+    def program(self):
+        return gen64.program(self.nw, self.kmask)
+
+    def render(self):
+        return gen64.render(self.nw, self.kmask)
 
 
 class _KMask:
@@ -58,8 +59,9 @@ class _KMask:
 
 
 # (generator, its .inc, the first Q register, Q registers)
-LOOPS = {"hd128": (gen, gen.INCS[False], gen.Q, 32), "hd128kmask": (_KMask, gen.INCS[True], gen.Q, 32),
-         "hd64": (gen64, gen64.INCS[4], gen64.Q, 16), "hd64w8": (_W8, gen64.INCS[8], gen64.Q, 16)}
+LOOPS = {"hd128": (gen, gen.INCS[False], gen.Q, 32), "hd128kmask": (_KMask, gen.INCS[True], gen.Q, 32)}
+LOOPS.update({f"hd64{'w8' if nw == 8 else ''}{'kmask' if km else ''}": (_G64(nw, km), inc, gen64.Q, 16)
+              for (nw, km), inc in gen64.INCS.items()})
 
 
 @pytest.mark.parametrize("loop", LOOPS)
@@ -78,8 +80,9 @@ def test_kernel_clobber_list_matches_the_generator(loop):
         d = src.rindex("#define TK_", 0, i)
         stmt = src[d:i]
     elif "_CLOBS" in stmt:  # outputs, inputs and clobbers are macros defined before the statements
-        d = src.rindex("#define TK_EPOCH_CLOBS", 0, i)
-        stmt = src[d:src.index("\n    if constexpr", d)] + stmt
+        name = re.search(r"(TK_\w+_CLOBS)", stmt).group(1)
+        d = src.rindex(f"#define {name}", 0, i)
+        stmt = src[d:src.index("if constexpr", d)] + stmt
     clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
     assert clobbers == g.CLOBBERED
     for extra in ('"vcc"', '"scc"', '"memory"'):
@@ -300,3 +303,28 @@ def test_key_masked_loop_adds_only_the_mask_work():
     i = src.index(f'#include "{gen.INCS[True]}"')
     clobs = src[i:src.index(");", i)]
     assert all(f'"s{r}"' in clobs for r in gen.S_CLOBBERED)
+
+
+@pytest.mark.parametrize("nw", [4, 8])
+def test_hd64_key_masked_loop_adds_only_the_mask_work(nw):
+    """The key-masked head_dim-64 loop keeps every instruction of the dense one in
+    order, except that the row max over a tile's scores moves from the step before
+    (into v160/v163, copied to T0 and T1) to after the selects that set masked
+    keys to -inf (straight into T0); it adds the byte load, key bits, the selects
+    and the m = -inf guard."""
+    dense, masked = gen64.program(nw, False), gen64.program(nw, True)
+    early = lambda l: l.startswith(("v_max3_f32 v160", "v_max_f32 v160", "v_max3_f32 v163", "v_max_f32 v163"))
+    late = lambda l: l.startswith(("v_max3_f32 v212", "v_max_f32 v212, v212, v1"))
+    copies = ("v_mov_b32 v212, v160", "v_mov_b32 v213, v160", "v_mov_b32 v212, v163", "v_mov_b32 v213, v163")
+    kept = [l for l in dense if not early(l) and l not in copies]
+    it = iter(masked)
+    assert all(any(m == l for m in it) for l in kept)
+    assert not any(map(early, masked))
+    scores = lambda prog, sel: sorted(int(r) for l in prog if sel(l) for r in re.findall(r"v(\d+)", l)[1:]
+                                      if int(r) not in (160, 163, 212))
+    assert scores(dense, early) == scores(masked, late) == [*range(112, 144), *range(164, 196)]
+    assert sum(1 for l in masked if l.startswith("s_bfe_i32")) == 2 * 2 * 32
+    src = (CSRC / "tk_attention.hip").read_text()
+    i = src.index(f'#include "{gen64.INCS[(nw, True)]}"')
+    clobs = src[i:src.index(");", i)]
+    assert all(f'"s{r}"' in clobs for r in gen64.KMASK_SGPRS)

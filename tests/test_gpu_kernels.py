@@ -443,16 +443,18 @@ def test_flash_attention_key_mask(shape, causal):
     assert not bool(torch.isfinite(out[~seen]).all()) or not bool((~seen).any())
 
 
+@pytest.mark.parametrize("hd", [64, 128])
 @pytest.mark.parametrize("pattern", ["tail", "head", "holes"])
-def test_flash_attention_key_masked_loop_is_bit_identical(pattern):
-    """head_dim 128, causal, with a key mask: the generated key-masked loop
-    (tk_attn_epochs_kmask.inc) against the compiled epochs, forced as in
+def test_flash_attention_key_masked_loop_is_bit_identical(pattern, hd):
+    """Causal with a key mask, head_dim 128 and 64: the generated key-masked loops
+    (tk_attn_epochs_kmask.inc, tk_attn_steps64_kmask.inc) against the compiled
+    epochs, forced as in
     test_flash_attention_epoch_loop_is_bit_identical by K/V rows 4 MiB apart.
     tail: padded keys at the end; head: the first 200 keys invalid, so query
     blocks enter the loop with rows that have seen no valid key (m = -inf);
     holes: about 30 % of keys invalid.  Rows with no valid key come out
     non-finite on both paths."""
-    b, h, s, hd = 2, 1, 1300, 128
+    b, h, s = 2, 1, 1300
     q, k, v = _qkv((b, h, s, hd), seed=97)
     kv = torch.ones(b, s, dtype=torch.bool)
     if pattern == "tail":

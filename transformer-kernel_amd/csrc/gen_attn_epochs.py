@@ -90,10 +90,11 @@ S_CLOBBERED = list(range(88, 96))
 NEG_INF = "0xff800000"
 
 
-def key_mask(sr) -> list[str]:
-    """Scores of keys whose validity byte is 0 -> -inf.  Entry i = 16*kb2 + r of a lane holds
-    key 32*kb2 + 8*(r/4) + r%4 + 4g (g = lane / 32), so its lane mask takes bit j of the tile's
-    bits for lanes 0..31 and bit j+4 for lanes 32..63 (s_bfe_i32 of one bit: 0 or -1)."""
+def key_mask(sr, neg: int = ALPHA) -> list[str]:
+    """Scores of keys whose validity byte is 0 -> -inf (held in register `neg`).  Entry
+    i = 16*kb2 + r of a lane holds key 32*kb2 + 8*(r/4) + r%4 + 4g (g = lane / 32), so its lane
+    mask takes bit j of the tile's bits (s92: keys 0..31, s93: 32..63) for lanes 0..31 and bit
+    j+4 for lanes 32..63 (s_bfe_i32 of one bit: 0 or -1)."""
     def mask(i: int, pair: int) -> list[str]:
         kb2, r = i >> 4, i & 15
         j = 32 * kb2 + 8 * (r >> 2) + (r & 3)
@@ -102,9 +103,9 @@ def key_mask(sr) -> list[str]:
                 f"s_bfe_i32 s{pair + 1}, s{S_KB[hi >> 5]}, {(hi & 31) | (1 << 16)}"]
 
     def select(i: int, pair: int) -> list[str]:
-        return [f"v_cndmask_b32 {v(sr(i))}, {v(ALPHA)}, {v(sr(i))}, s[{pair}:{pair + 1}]"]
+        return [f"v_cndmask_b32 {v(sr(i))}, {v(neg)}, {v(sr(i))}, s[{pair}:{pair + 1}]"]
 
-    out = [f"v_mov_b32 {v(ALPHA)}, {NEG_INF}"] + mask(0, S_MASK[0])
+    out = [f"v_mov_b32 {v(neg)}, {NEG_INF}"] + mask(0, S_MASK[0])
     for i in range(32):
         if i + 1 < 32:
             out += mask(i + 1, S_MASK[(i + 1) % 2])  # two instructions between a mask and its use

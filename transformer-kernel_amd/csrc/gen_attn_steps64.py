@@ -52,6 +52,9 @@ from __future__ import annotations
 import pathlib
 import sys
 
+sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent))
+from gen_attn_epochs import NEG_INF, S_CLOBBERED, S_KB, S_NOKEY, key_mask  # noqa: E402
+
 O = 64
 Q = 96
 X, W, MXX = 112, 144, 160
@@ -72,10 +75,16 @@ def v(a: int, n: int = 1) -> str:
     return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
 
 
-def step(par: int, nw: int = 4) -> list[str]:
+def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
     """One step of an nw-wave workgroup (4: two 1 KB copies per tile and wave, 8: one);
     par 0: scores X current, Y next, P W previous, Z new; par 1 swaps them.
-    Step kt has par = (kt + 1) % 2 (the loop starts at kt = 1)."""
+    Step kt has par = (kt + 1) % 2 (the loop starts at kt = 1).
+
+    kmask (key-validity mask): like the compiled key-masked step, the row max of S(kt) is taken
+    over its scores after the invalid keys' scores are set to -inf (s92/s93 hold tile kt's key
+    bits), so the next tile's running max is not kept, and its register takes the next tile's
+    validity bytes (loaded at the start of the step, turned into key bits after its copy wait);
+    rows with no valid key yet exponentiate against 0 and keep m = -inf."""
     s_cur, s_nxt = (X, Y) if par == 0 else (Y, X)
     p_prev, p_cur = (W, Z) if par == 0 else (Z, W)
     mx_cur, mx_nxt = (MXX, MXY) if par == 0 else (MXY, MXX)
@@ -83,8 +92,18 @@ def step(par: int, nw: int = 4) -> list[str]:
     k_wr = (1 - par) * TILE               # K(kt+2) is written into slot kt % 2
 
     L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    if kmask:
+        L += [f"global_load_ubyte {v(mx_nxt)}, %[koff], %[kvb]", "v_add_u32 %[koff], 64, %[koff]"]
     # ---- row max of S(kt) over the lane pair, lazy rescale ----
-    L += [f"v_mov_b32 {v(TMP)}, {v(mx_cur)}", f"v_mov_b32 {v(MX)}, {v(mx_cur)}", "s_nop 1",
+    if kmask:
+        L += key_mask(lambda i: s_cur + i, ALPHA)
+        L.append(f"v_max3_f32 {v(MX)}, {v(s_cur)}, {v(s_cur + 1)}, {v(s_cur + 2)}")
+        for k in range(3, 31, 2):
+            L.append(f"v_max3_f32 {v(MX)}, {v(MX)}, {v(s_cur + k)}, {v(s_cur + k + 1)}")
+        L += [f"v_max_f32 {v(MX)}, {v(MX)}, {v(s_cur + 31)}", f"v_mov_b32 {v(TMP)}, {v(MX)}"]
+    else:
+        L += [f"v_mov_b32 {v(TMP)}, {v(mx_cur)}", f"v_mov_b32 {v(MX)}, {v(mx_cur)}"]
+    L += ["s_nop 1",
           f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
           f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
           f"v_mul_f32 {v(MX)}, {v(MX)}, %[cs]",                  # m_tile
@@ -98,6 +117,9 @@ def step(par: int, nw: int = 4) -> list[str]:
           f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
           "s_mov_b32 %[flag], 1"]
     L += [f"L_norescale_{par}_%=:"]
+    if kmask:  # rows with no valid key so far: exponentials against 0, m_run restored after
+        L += [f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(MR)}", f"s_mov_b64 s[{S_NOKEY}:{S_NOKEY + 1}], vcc",
+              f"v_cndmask_b32 {v(MR)}, {v(MR)}, 0, vcc"]
     # ---- fragment reads: slot m's fragment into ring entry m % 3; read addresses go
     # through the exponential pair that is idle where the read is issued (ka) ----
     def reads(m: int, ka: int = -1) -> list[str]:
@@ -190,7 +212,8 @@ def step(par: int, nw: int = 4) -> list[str]:
         L += expo(m)
         L += scale(m + 1) if m + 1 < 16 else ["s_nop 1"]
         L += pack(m)
-        L += nmax(m)
+        if not kmask:
+            L += nmax(m)
         if m == 0:
             L += kcopy
         if m == 2:
@@ -200,8 +223,15 @@ def step(par: int, nw: int = 4) -> list[str]:
     L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{par}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
     L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(32)]
     L += [f"L_noscale_{par}_%=:"]
+    if kmask:
+        L += [f"v_mov_b32 {v(ALPHA)}, {NEG_INF}",
+              f"v_cndmask_b32 {v(MR)}, {v(MR)}, {v(ALPHA)}, s[{S_NOKEY}:{S_NOKEY + 1}]"]
     # ---- end: this step's copies have landed; barrier; next V slots ----
-    L += ["s_waitcnt vmcnt(0) lgkmcnt(0)", "s_barrier",
+    L += ["s_waitcnt vmcnt(0) lgkmcnt(0)"]
+    if kmask:  # the next tile's key bits
+        L += [f"v_cmp_ne_u32 vcc, 0, {v(mx_nxt)}", f"s_mov_b32 s{S_KB[0]}, vcc_lo",
+              f"s_mov_b32 s{S_KB[1]}, vcc_hi"]
+    L += ["s_barrier",
           f"s_add_u32 %[vrd], %[vrd], {TILE}", f"s_cmp_eq_u32 %[vrd], {VSLOTS * TILE}",
           "s_cselect_b32 %[vrd], 0, %[vrd]",
           f"s_add_u32 %[vwr], %[vwr], {TILE}", f"s_cmp_eq_u32 %[vwr], {VSLOTS * TILE}",
@@ -209,33 +239,37 @@ def step(par: int, nw: int = 4) -> list[str]:
     return L
 
 
-def program(nw: int = 4) -> list[str]:
+def program(nw: int = 4, kmask: bool = False) -> list[str]:
     """M0 saved, `groups` iterations of two steps, M0 restored."""
     # the scores and P tile handed in were written by MFMAs and VALU ops of the compiled code
     L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    if kmask:  # key bits of tile 1, from the compiled step 0
+        L += [f"s_mov_b64 s[{S_KB[0]}:{S_KB[1]}], %[kbits]"]
     L += ["L_steps_%=:"]
-    L += step(0, nw) + step(1, nw)
+    L += step(0, nw, kmask) + step(1, nw, kmask)
     L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_steps_%="]
     # the compiled code after the statement reads O and the scores: MFMA result latency first
     L += ["s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
     return L
 
 
-INCS = {4: "tk_attn_steps64.inc", 8: "tk_attn_steps64_w8.inc"}
-INC = INCS[4]
+INCS = {(4, False): "tk_attn_steps64.inc", (8, False): "tk_attn_steps64_w8.inc",
+        (4, True): "tk_attn_steps64_kmask.inc", (8, True): "tk_attn_steps64_w8_kmask.inc"}
+INC = INCS[(4, False)]
+KMASK_SGPRS = S_CLOBBERED
 
 
-def render(nw: int = 4) -> str:
-    head = f"// Generated by gen_attn_steps64.py ({nw} waves); do not edit.\n"
-    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program(nw))
+def render(nw: int = 4, kmask: bool = False) -> str:
+    head = f"// Generated by gen_attn_steps64.py ({nw} waves{', key-masked' if kmask else ''}); do not edit.\n"
+    body = "\n".join(f'"{l}\\n"' if l.endswith(":") else f'"{l}\\n\\t"' for l in program(nw, kmask))
     return head + body + "\n"
 
 
 def write(directory: pathlib.Path | None = None) -> list[pathlib.Path]:
     paths = []
-    for nw, name in INCS.items():
+    for (nw, kmask), name in INCS.items():
         path = (directory or pathlib.Path(__file__).resolve().parent) / name
-        text = render(nw)
+        text = render(nw, kmask)
         if not path.exists() or path.read_text() != text:
             path.write_text(text)
         paths.append(path)
@@ -243,6 +277,6 @@ def write(directory: pathlib.Path | None = None) -> list[pathlib.Path]:
 
 
 if __name__ == "__main__":
-    for out, nw in zip(write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None), INCS):
-        prog = program(nw)
+    for out, (nw, kmask) in zip(write(pathlib.Path(sys.argv[1]) if len(sys.argv) > 1 else None), INCS):
+        prog = program(nw, kmask)
         print(out, len(prog), "lines", sum(1 for l in prog if l.startswith("v_mfma")), "MFMAs")

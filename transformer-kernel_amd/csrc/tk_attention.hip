@@ -412,7 +412,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   // copies use 32-bit offsets from the K and V bases (span check) and the K read
   // addresses are formed by XOR on bits 5-6 of a 256-byte-aligned row offset.
   int groups = 0;
-  if constexpr (HD == 64 && (NW == 4 || NW == 8) && CAUSAL && !KMASK) {
+  if constexpr (HD == 64 && (NW == 4 || NW == 8) && CAUSAL) {
     const int last = min(q0 / kBN - 1, min(n_kt, p.S / kBN) - 3);
     const int64_t span =
         ((int64_t)n_kt + 2) * max(k_tile, v_tile) * 2 + (int64_t)kBN * max(p.ks[2], p.vs[2]) * 2;
@@ -429,7 +429,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     // Two steps per iteration with no branch between them: the loop-carried
     // accumulators then keep one register assignment.
     int kt = 1;
-    if constexpr (HD == 64 && (NW == 4 || NW == 8) && CAUSAL && !KMASK) {
+    if constexpr (HD == 64 && (NW == 4 || NW == 8) && CAUSAL) {
       if (groups > 0) {
         // Pinned: O^T v[64:95], Q v[96:111], the scores of tile kt v[112:143] (s_b), P of
         // tile kt-1 v[144:159] (pf_a), their row max v160 (mx_b), m_run v161, l_run v162.
@@ -449,35 +449,58 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
         const float cs = p.scale_log2;
         uint32_t vrd = 0, vwr = 2 * TILE;  // step 1 reads V(0) from V slot 0, writes V(2) into slot 2
         uint32_t msave, cnt, flag;
-#define TK_STEPS64_OPERANDS \
-            : [o0] "+{v[64:79]}"(acc_o[0]), [o1] "+{v[80:95]}"(acc_o[1]), [x0] "+{v[112:127]}"(s_b[0]), \
-              [x1] "+{v[128:143]}"(s_b[1]), [w0] "+{v[144:147]}"(pf_a[0]), [w1] "+{v[148:151]}"(pf_a[1]), \
-              [w2] "+{v[152:155]}"(pf_a[2]), [w3] "+{v[156:159]}"(pf_a[3]), [mxx] "+{v160}"(mx_b), \
-              [mr] "+{v161}"(m_run), [lr] "+{v162}"(l_run), [ko0] "+&v"(ko[0]), [ko1] "+&v"(ko[1]), \
-              [vo0] "+&v"(vo[0]), [vo1] "+&v"(vo[1]), [vrd] "+&s"(vrd), [vwr] "+&s"(vwr), \
-              [msave] "=&s"(msave), [cnt] "=&s"(cnt), [flag] "=&s"(flag) \
-            : [q0] "{v[96:99]}"(qf[0]), [q1] "{v[100:103]}"(qf[1]), [q2] "{v[104:107]}"(qf[2]), \
-              [q3] "{v[108:111]}"(qf[3]), [kl0] "v"(kl0), [vl0] "v"(vl0), [vl1] "v"(vl1), [kb] "s"(kb), \
-              [vb] "s"(vb), [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), [cs] "s"(cs), \
-              [groups] "s"(groups) \
-            : "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
-              "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", \
-              "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", \
-              "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", \
-              "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", \
-              "v223", "v224", "v225", "v226", "v227", "v228", "v229", \
-              "vcc", "scc", "memory"
-        if constexpr (NW == 4) {
+#define TK_STEPS64_OUTS \
+          [o0] "+{v[64:79]}"(acc_o[0]), [o1] "+{v[80:95]}"(acc_o[1]), [x0] "+{v[112:127]}"(s_b[0]), [x1] "+{v[128:143]}"(s_b[1]), \
+          [w0] "+{v[144:147]}"(pf_a[0]), [w1] "+{v[148:151]}"(pf_a[1]), [w2] "+{v[152:155]}"(pf_a[2]), [w3] "+{v[156:159]}"(pf_a[3]), \
+          [mxx] "+{v160}"(mx_b), [mr] "+{v161}"(m_run), [lr] "+{v162}"(l_run), [ko0] "+&v"(ko[0]), \
+          [ko1] "+&v"(ko[1]), [vo0] "+&v"(vo[0]), [vo1] "+&v"(vo[1]), [vrd] "+&s"(vrd), \
+          [vwr] "+&s"(vwr), [msave] "=&s"(msave), [cnt] "=&s"(cnt), [flag] "=&s"(flag)
+#define TK_STEPS64_INS \
+          [q0] "{v[96:99]}"(qf[0]), [q1] "{v[100:103]}"(qf[1]), [q2] "{v[104:107]}"(qf[2]), [q3] "{v[108:111]}"(qf[3]), \
+          [kl0] "v"(kl0), [vl0] "v"(vl0), [vl1] "v"(vl1), [kb] "s"(kb), \
+          [vb] "s"(vb), [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), \
+          [cs] "s"(cs), [groups] "s"(groups)
+#define TK_STEPS64_CLOBS \
+          "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
+          "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", \
+          "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", \
+          "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", \
+          "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", \
+          "v223", "v224", "v225", "v226", "v227", "v228", "v229", "vcc", "scc", "memory"
+        if constexpr (KMASK) {
+          // the validity byte of key 64(kt+1) + lane is read in step kt, from kt = 1
+          uint32_t koff = lane + 2 * kBN;
+          if constexpr (NW == 4) {
+            asm volatile(
+#include "tk_attn_steps64_kmask.inc"
+                : TK_STEPS64_OUTS, [koff] "+&v"(koff)
+                : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
+                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+          } else {
+            asm volatile(
+#include "tk_attn_steps64_w8_kmask.inc"
+                : TK_STEPS64_OUTS, [koff] "+&v"(koff)
+                : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
+                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+          }
+        } else if constexpr (NW == 4) {
           asm volatile(
 #include "tk_attn_steps64.inc"
-              TK_STEPS64_OPERANDS);
+              : TK_STEPS64_OUTS
+              : TK_STEPS64_INS
+              : TK_STEPS64_CLOBS);
         } else {
           asm volatile(
 #include "tk_attn_steps64_w8.inc"
-              TK_STEPS64_OPERANDS);
+              : TK_STEPS64_OUTS
+              : TK_STEPS64_INS
+              : TK_STEPS64_CLOBS);
         }
-#undef TK_STEPS64_OPERANDS
+#undef TK_STEPS64_OUTS
+#undef TK_STEPS64_INS
+#undef TK_STEPS64_CLOBS
         kt += 2 * groups;
+        if constexpr (KMASK) kbits_cur = (uint64_t)__ballot(key_byte(kt) != 0);  // the loop keeps its own
       }
       // the copy addresses are rebuilt rather than kept live across the asm loop
       int ln = lane;
