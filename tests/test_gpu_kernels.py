@@ -483,6 +483,32 @@ def test_flash_attention_key_masked_loop_is_bit_identical(pattern, hd):
     assert bad == 0, err
 
 
+def test_flash_attention_key_mask_256_row_blocks():
+    """Causal head_dim 64 beyond 32768 keys runs 256-row query blocks (8 waves),
+    whose key-masked steps come from tk_attn_steps64_w8_kmask.inc.  Padded tail
+    (batch 0 from key 30000) and ~20 % random holes; sampled query rows (block
+    edges, the padded tail, random rows) against the masked baseline softmax
+    (src/torch_transformer_benchmark.py:97-112) over each row's full key range."""
+    b, h, s, hd = 2, 2, 33000, 64
+    q, k, v = _qkv((b, h, s, hd), seed=33)
+    g = torch.Generator().manual_seed(7)
+    kv = torch.rand(b, s, generator=g) > 0.2
+    kv[0, 30000:] = False
+    out = ops.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5, True, key_valid=kv.to(DEV)).cpu()
+    rows = torch.unique(torch.cat([torch.tensor([0, 1, 255, 256, 511, 16383, 32767, 32768, 29999, 30000, s - 2, s - 1]),
+                                   torch.randint(0, s, (116,), generator=g)]))
+    for bi in range(b):
+        for hi in range(h):
+            scores = torch.matmul(q[bi, hi, rows].float(), k[bi, hi].float().t()) * hd ** -0.5
+            allowed = kv[bi][None, :] & (torch.arange(s)[None, :] <= rows[:, None])
+            ref = torch.matmul(ob.masked_softmax_ref(scores, False, allowed), v[bi, hi].float())
+            got = out[bi, rows, hi * hd:(hi + 1) * hd]
+            seen = allowed.any(-1)
+            bad, err = or_rule_violations(got[seen], ref[seen])
+            assert bad == 0, (bi, hi, err)
+            assert not bool(torch.isfinite(got[~seen]).any())
+
+
 def test_attention_support_probes():
     """The reference's rule, next_pow2(max(hd, 16)) <= 256 for fp16 on the GPU
     (src/kernels.py:96-103); above it the kernel raises."""
