@@ -137,13 +137,13 @@ struct Mainloop {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   }
 
-  __device__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+  __device__ __forceinline__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     zero(acc);
     if constexpr (DIRECT) run_direct(p, m0, n0, smem, acc);
     else run_staged(p, m0, n0, smem, acc);
   }
 
-  __device__ static void run_direct(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+  __device__ __forceinline__ static void run_direct(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave % WAVES_M;
@@ -259,7 +259,7 @@ struct Mainloop {
     }
   }
 
-  __device__ static void run_staged(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
+  __device__ __forceinline__ static void run_staged(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -382,27 +382,25 @@ __device__ __forceinline__ int epi_off(int row, int chunk) {
 }
 
 // Residual epilogue with per-row validity (padded rows, tk_row_mode): an
-// internal epilogue code, picked when row_valid is given.
+// internal epilogue code, picked when row_valid is given; it runs the
+// residual epilogue's passes with the per-row select.
 constexpr int kEpiResidRows = 3;
 
-// Each wave stages its WM x WN result tile (in rows of 32 x JC) in its own LDS
-// region, row-major, then reads it back 16 bytes per lane along rows: every
-// global store, and every fp32 residual load, then covers whole 128-byte
-// lines instead of 16-byte pieces of 32 rows.  Bias and GELU are applied in
-// fp32 before the fp16 rounding; the padded-row residual epilogue
-// (kEpiResidRows) adds bias and residual on the read-back side.
+// Each wave stages its WM x WN fp16 result tile (in rows of 32 x JC) in its
+// own LDS region, row-major, then reads it back 16 bytes per lane along rows:
+// every global store then covers whole 128-byte lines instead of 16-byte
+// pieces of 32 rows.  Bias and GELU are applied in fp32 before the fp16
+// rounding.
 template <class ML, int WAVES_M, int EPI>
 __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                int n0, f16* smem) {
-  constexpr bool F32 = EPI == kEpiResidRows;
-  constexpr int ES = F32 ? 4 : 2;
   constexpr int WM = ML::WM, WN = ML::WN, FM = ML::FM, FN = ML::FN, NW = ML::NW;
-  constexpr int ROWB = WN * ES;
+  constexpr int ROWB = WN * 2;
   constexpr int CPR = ROWB / 16;
   constexpr int LDS_BYTES = ML::LDS_HALVES * 2;
   constexpr int JC = (NW * FM * 32 * ROWB <= LDS_BYTES) ? FM : (NW * 32 * ROWB <= LDS_BYTES ? 1 : 0);
   static_assert(JC > 0 && FM % JC == 0, "staging region does not fit");
-  constexpr int EPC = 16 / ES;  // elements per chunk
+  constexpr int EPC = 8;  // elements per chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int mw = m0 + (wave % WAVES_M) * WM;
   const int nw = n0 + (wave / WAVES_M) * WN;
@@ -416,35 +414,28 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
       for (int q = 0; q < 4; ++q) {
         const int nl = i * 32 + 8 * q + 4 * (lane >> 5);  // 4 consecutive n of this lane
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (!F32) {
-          const int n = nw + nl;
-          if (p.bias) {
-            if (p.bias16 && n + 3 < p.N) {
-              const f32x4 b4 = *reinterpret_cast<const f32x4*>(p.bias + n);
-              bv[0] = b4[0]; bv[1] = b4[1]; bv[2] = b4[2]; bv[3] = b4[3];
-            } else {
+        const int n = nw + nl;
+        if (p.bias) {
+          if (p.bias16 && n + 3 < p.N) {
+            const f32x4 b4 = *reinterpret_cast<const f32x4*>(p.bias + n);
+            bv[0] = b4[0]; bv[1] = b4[1]; bv[2] = b4[2]; bv[3] = b4[3];
+          } else {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) bv[e] = n + e < p.N ? p.bias[n + e] : 0.f;
-            }
+            for (int e = 0; e < 4; ++e) bv[e] = n + e < p.N ? p.bias[n + e] : 0.f;
           }
         }
 #pragma unroll
         for (int jj = 0; jj < JC; ++jj) {
           const int row = jj * 32 + (lane & 31);
           const f32x16& a = acc[i][jb + jj];
-          if constexpr (F32) {
-            *reinterpret_cast<f32x4*>(region + epi_off<CPR>(row, nl / 4)) =
-                f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-          } else {
-            float v[4];
+          float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = a[4 * q + e] + bv[e];
-              if constexpr (EPI == TK_EPI_BIAS_GELU) v[e] = gelu_erf(v[e]);
-            }
-            *reinterpret_cast<f16x4*>(region + epi_off<CPR>(row, nl / 8) + (nl % 8) * 2) =
-                f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          for (int e = 0; e < 4; ++e) {
+            v[e] = a[4 * q + e] + bv[e];
+            if constexpr (EPI == TK_EPI_BIAS_GELU) v[e] = gelu_erf(v[e]);
           }
+          *reinterpret_cast<f16x4*>(region + epi_off<CPR>(row, nl / 8) + (nl % 8) * 2) =
+              f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
         }
       }
     }
@@ -460,38 +451,13 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
       const int row = idx / CPR, ch = idx % CPR;
       const int m = mw + jb * 32 + row;
       const int n = nw + ch * EPC;
-      const char* src = region + epi_off<CPR>(row, ch);
       if (m < p.M && n < p.N) {
-        if constexpr (F32) {
-          const f32x4 d = *reinterpret_cast<const f32x4*>(src);
-          const float* rr = p.resid + (int64_t)m * p.ldr + n;
-          float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
-          // padded row: the product counts as 0 (keep resid) or the row is 0
-          const bool valid = p.row_valid == nullptr || p.row_valid[m] != 0;
-          const bool keep = p.row_mode == TK_ROWS_KEEP_RESID;
-          if (p.vec && n + 3 < p.N) {
-            const f32x4 r = *reinterpret_cast<const f32x4*>(rr);
-            f32x4 b = {0.f, 0.f, 0.f, 0.f};
-            if (p.bias) {
-              if (p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
-              else b = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
-            }
-            f32x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = valid ? r[e] + (d[e] + b[e]) : (keep ? r[e] : 0.f);
-            *reinterpret_cast<f32x4*>(cr) = o;
-          } else {
-            for (int e = 0; e < 4 && n + e < p.N; ++e)
-              cr[e] = valid ? rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f)) : (keep ? rr[e] : 0.f);
-          }
+        const f16x8 d = *reinterpret_cast<const f16x8*>(region + epi_off<CPR>(row, ch));
+        f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
+        if (p.vec && n + 7 < p.N) {
+          *reinterpret_cast<f16x8*>(cr) = d;
         } else {
-          const f16x8 d = *reinterpret_cast<const f16x8*>(src);
-          f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
-          if (p.vec && n + 7 < p.N) {
-            *reinterpret_cast<f16x8*>(cr) = d;
-          } else {
-            for (int e = 0; e < 8 && n + e < p.N; ++e) cr[e] = d[e];
-          }
+          for (int e = 0; e < 8 && n + e < p.N; ++e) cr[e] = d[e];
         }
       }
     }
@@ -508,10 +474,11 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
 // accumulators are staged in LDS, when the accumulator blocks still live in
 // the pass leave room (at most 64 registers), else 8 after the staging.  In the row-major read-back a lane always
 // lands on the same 16-byte column chunk (64 lanes cover 64 / CPR whole
-// rows), so its bias is one vector.  Launches with padded rows (row_valid)
-// take the kEpiResidRows path of store_tile_lds instead: the per-row
-// validity selects do not fit next to the prefetched rows in 256 registers.
-template <class ML, int WAVES_M, int JB, int JC>
+// rows), so its bias is one vector.  With padded rows (ROWS: row_valid
+// given) the pass's JC * 32 validity bytes are loaded once, one per lane, and
+// their ballot is a wave-uniform bit mask; a lane tests its row's bit, and
+// an invalid row is written as resid (TK_ROWS_KEEP_RESID) or 0.
+template <class ML, int WAVES_M, int JB, int JC, bool ROWS>
 __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int mw, int nw,
                                            char* region) {
   constexpr int FN = ML::FN;
@@ -529,6 +496,13 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
   // wave-uniform base + 32-bit lane offsets (a pass spans 32 rows)
   const float* rbase = p.resid + (int64_t)mb * p.ldr + nw;
   const uint32_t ldr = (uint32_t)p.ldr;
+  uint64_t rows_ok = ~0ull;  // bit r: row mb + r is valid
+  const bool keep = p.row_mode == TK_ROWS_KEEP_RESID;
+  static_assert(JC * 32 <= 64, "one validity bit per lane");
+  if constexpr (ROWS) {
+    const int m = mb + lane;
+    rows_ok = __ballot(lane < JC * 32 && m < p.M && p.row_valid[m] != 0);
+  }
 
   f32x4 r[G];
   auto fetch = [&](int g) {
@@ -547,15 +521,16 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
       if (m < p.M && n < p.N) {
         const f32x4 d = *reinterpret_cast<const f32x4*>(region + epi_off<CPR>(row, ch));
         float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
+        const bool valid = !ROWS || ((rows_ok >> row) & 1ull);
         if (vec) {
           f32x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = r[it][e] + (d[e] + b[e]);
+          for (int e = 0; e < 4; ++e) o[e] = valid ? r[it][e] + (d[e] + b[e]) : (keep ? r[it][e] : 0.f);
           *reinterpret_cast<f32x4*>(cr) = o;
         } else {
           const float* rr = p.resid + (int64_t)m * p.ldr + n;
           for (int e = 0; e < 4 && n + e < p.N; ++e)
-            cr[e] = rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f));
+            cr[e] = valid ? rr[e] + (d[e] + (p.bias ? p.bias[n + e] : 0.f)) : (keep ? rr[e] : 0.f);
         }
       }
     }
@@ -592,7 +567,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
 
 // fp32 residual epilogue: one resid_pass per group of JC accumulator blocks
 // (two groups when the staging region holds one 32-row block per wave).
-template <class ML, int WAVES_M>
+template <class ML, int WAVES_M, bool ROWS>
 __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                  int n0, f16* smem) {
   constexpr int FM = ML::FM, NW = ML::NW;
@@ -605,8 +580,8 @@ __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16
   const int nw = n0 + (wave / WAVES_M) * ML::WN;
   char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
   __syncthreads();  // every wave is done with the main-loop buffers
-  resid_pass<ML, WAVES_M, 0, JC>(p, acc, mw, nw, region);
-  if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC>(p, acc, mw, nw, region);
+  resid_pass<ML, WAVES_M, 0, JC, ROWS>(p, acc, mw, nw, region);
+  if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC, ROWS>(p, acc, mw, nw, region);
 }
 
 template <class T, int EPI, bool DIRECT>
@@ -620,8 +595,8 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   f32x16 acc[ML::FN][ML::FM];
   ML::run(p, tm * BM, tn * BN, smem, acc);
-  if constexpr (EPI == TK_EPI_BIAS_RESID)
-    store_tile_resid<ML, T::WAVES_M>(p, acc, tm * BM, tn * BN, smem);
+  if constexpr (EPI == TK_EPI_BIAS_RESID || EPI == kEpiResidRows)
+    store_tile_resid<ML, T::WAVES_M, EPI == kEpiResidRows>(p, acc, tm * BM, tn * BN, smem);
   else
     store_tile_lds<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem);
 }
