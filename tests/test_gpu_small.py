@@ -6,8 +6,10 @@ width 128 with head_dim 16/32/64/128, causal and not) against
     (src/torch_transformer_benchmark.py:309-316);
   * the layer-by-layer HIP path on the same weights and input (same
     arithmetic, different fp16 rounding points -- LayerNorm sums, and P
-    rounded per 32-key block here against the layer path's key tiles:
-    within 2e-3).
+    rounded per 32-key block here against the layer path's key tiles):
+    within 1e-3 of each other (measured at most 6.3e-4 over these shapes),
+    and the whole-forward kernel's worst error against the oracle no more
+    than 1e-4 above the layer path's (measured at most 2e-5 above).
 A padded input, and a shape outside the envelope, take the layer path.
 """
 
@@ -60,10 +62,14 @@ def test_small_forward_parity(shape):
     with torch.no_grad():
         ref = base(x)
     res = ob.compare_outputs(ref, got.cpu())
-    print(f"{shape}: max_abs={res.max_abs_error:.3g} failed={res.failed_elements}", flush=True)
+    res_layered = ob.compare_outputs(ref, layered.cpu())
+    between = (got - layered).abs().max().item()
+    print(f"{shape}: max_abs={res.max_abs_error:.3g} layered={res_layered.max_abs_error:.3g} "
+          f"between={between:.3g} failed={res.failed_elements}", flush=True)
     assert res.passed, (res.max_abs_error, res.failed_elements)
     assert torch.isfinite(got).all()
-    assert (got - layered).abs().max().item() <= 2e-3
+    assert between <= 1e-3
+    assert res.max_abs_error <= res_layered.max_abs_error + 1e-4
 
 
 def test_small_forward_is_deterministic_and_batch_independent():
