@@ -472,7 +472,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
 // residual rows a lane combines (16 rows of 16 bytes per pass) are loaded
 // in groups of G with one wait per group: all 16 at once, issued before the
 // accumulators are staged in LDS, when the accumulator blocks still live in
-// the pass leave room (at most 64 registers), else 8 after the staging.  In the row-major read-back a lane always
+// the pass leave room (at most 128 registers; 64 with padded rows, whose
+// row-bit handling needs the rest), else 8 after the staging.  On the
+// 256x256 tile the early group takes the kernel to 252 VGPRs at two waves
+// per SIMD, without scratch.  In the row-major read-back a lane always
 // lands on the same 16-byte column chunk (64 lanes cover 64 / CPR whole
 // rows), so its bias is one vector.  With padded rows (ROWS: row_valid
 // given) the pass's JC * 32 validity bytes are loaded once, one per lane, and
@@ -485,7 +488,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
   constexpr int CPR = ML::WN * 4 / 16;  // 16-byte chunks per staged row
   constexpr int RPI = 64 / CPR;         // staged rows per read-back step of the wave
   constexpr int NIT = JC * 32 / RPI;    // read-back steps of the pass
-  constexpr bool EARLY = FN * (ML::FM - JB) * 16 <= 64;
+  constexpr bool EARLY = FN * (ML::FM - JB) * 16 <= (ROWS ? 64 : 128);
   constexpr int G = EARLY ? NIT : NIT / 2;  // rows per load group
   static_assert(64 % CPR == 0 && (JC * 32) % RPI == 0 && NIT % G == 0, "whole rows per read-back step");
   const int lane = threadIdx.x & 63;
