@@ -80,36 +80,64 @@ def cpu_cores() -> int:
     return max(1, n)
 
 
-def kernel_units(name: str, cfg) -> tuple:
-    """(algorithmic amount per launch, unit, bound) for a kernel role."""
-    b, s, d, h, f, _, causal = cfg
+def kernel_units(name: str, cfg) -> dict:
+    """Algorithmic work of one launch of a kernel role: {"flop": F, "byte": B}.
+
+    Each unit present is priced against its roof (fp16 MFMA peak, HBM
+    bandwidth); the role is bound by whichever roof takes longer.  Bytes are
+    the launch's compulsory HBM traffic: every operand read once and every
+    output written once (fp16 GEMM operands and outputs 2 B/element, an fp32
+    residual read 4 + sum write 4 B/element, the fused residual + LayerNorm
+    epilogue 4 + 4 + 2).
+    """
+    b, s, d, h, f, nl, causal = cfg
     t = b * s
+    pairs = s * (s + 1) / 2 if causal else s * s
+    # (M, N, K, output bytes per element) of each GEMM role
     gemm = {
-        "qkv": 2.0 * t * 3 * d * d,
-        "out_proj_ln": 2.0 * t * d * d,
-        "out_proj_resid": 2.0 * t * d * d,
-        "ffn_up_gelu": 2.0 * t * f * d,
-        "ffn_down_ln": 2.0 * t * d * f,
-        "ffn_down_resid": 2.0 * t * d * f,
+        "qkv": (t, 3 * d, d, 2),
+        "out_proj_ln": (t, d, d, 10),
+        "out_proj_resid": (t, d, d, 8),
+        "ffn_up_gelu": (t, f, d, 2),
+        "ffn_down_ln": (t, d, f, 10),
+        "ffn_down_resid": (t, d, f, 8),
     }
     if name in gemm:
-        return gemm[name], "flop", "mfma"
+        m, n, k, ob = gemm[name]
+        return {"flop": 2.0 * m * n * k, "byte": 2.0 * (m * k + n * k) + 4.0 * n + float(ob) * m * n}
     if name == "small_forward":  # the whole forward (every layer) in one launch
-        pairs = s * (s + 1) / 2 if causal else s * s
         per_layer = 2.0 * t * (3 * d * d + d * d + 2 * d * f) + 4.0 * b * d * pairs
-        return per_layer * cfg[5], "flop", "mfma"
-    if name == "qkv_attn":  # fused QKV projection + one-tile attention
-        pairs = s * (s + 1) / 2 if causal else s * s
-        return 2.0 * t * 3 * d * d + 4.0 * b * d * pairs, "flop", "mfma"
-    if name == "flash_attn":
-        if s <= 64:  # one key tile per head: Q, K, V read and O written once (fp16)
-            return 8.0 * t * d, "byte", "hbm"
-        pairs = s * (s + 1) / 2 if causal else s * s
-        return 4.0 * b * d * pairs, "flop", "mfma"
+        return {"flop": per_layer * nl}
+    if name == "qkv_attn":  # fused QKV projection + one-tile attention: h and W in, ctx out
+        return {"flop": 2.0 * t * 3 * d * d + 4.0 * b * d * pairs, "byte": 2.0 * t * d * 2 + 2.0 * 3 * d * d}
+    if name == "flash_attn":  # Q, K, V read and the context written once (fp16)
+        return {"flop": 4.0 * b * d * pairs, "byte": 8.0 * t * d}
     ln_bytes = {"ln_in": 6, "ln2": 6, "ln_next": 6, "ln_final": 8}
     if name in ln_bytes:
-        return float(ln_bytes[name] * t * d), "byte", "hbm"
+        return {"byte": float(ln_bytes[name] * t * d)}
     raise KeyError(name)
+
+
+def kernel_roofline(name: str, cfg, avg_ms: float) -> dict:
+    """Both roofline fractions of a role's average launch and the binding one."""
+    units = kernel_units(name, cfg)
+    secs = avg_ms * 1e-3
+    out = {}
+    if "flop" in units:
+        out["flop_per_launch"] = units["flop"]
+        out["frac_mfma"] = round(units["flop"] / secs / (PEAK_FP16_TFLOPS * 1e12), 4)
+    if "byte" in units:
+        out["bytes_per_launch"] = units["byte"]
+        out["frac_hbm"] = round(units["byte"] / secs / (PEAK_HBM_GBPS * 1e9), 4)
+    t_mfma = units.get("flop", 0.0) / (PEAK_FP16_TFLOPS * 1e12)
+    t_hbm = units.get("byte", 0.0) / (PEAK_HBM_GBPS * 1e9)
+    if t_mfma >= t_hbm:
+        out.update(bound="mfma", achieved=round(units["flop"] / secs / 1e12, 2), unit="TFLOP/s",
+                   frac=out["frac_mfma"], algorithmic_per_launch=units["flop"], algorithmic_unit="flop")
+    else:
+        out.update(bound="hbm", achieved=round(units["byte"] / secs / 1e9, 2), unit="GB/s",
+                   frac=out["frac_hbm"], algorithmic_per_launch=units["byte"], algorithmic_unit="byte")
+    return out
 
 
 COPY_BYTES = 512 * 1024 * 1024  # per direction
@@ -136,6 +164,73 @@ def measured_traffic(config: str, kernel: str):
         return None
     entry = table.get("kernels", {}).get(config, {}).get(kernel)
     return None if entry is None else entry.get("bytes_per_launch")
+
+
+# GEMM roles of one layer: (M, N, K, epilogue) for a config
+def gemm_roles(cfg) -> dict:
+    b, s, d, h, f, _, _ = cfg
+    t = b * s
+    return {"qkv": (t, 3 * d, d, "bias"), "out_proj_resid": (t, d, d, "resid"),
+            "ffn_up_gelu": (t, f, d, "gelu"), "ffn_down_resid": (t, d, f, "resid")}
+
+
+def gemm_yardstick(configs, reps: int) -> int:
+    """Time this build's GEMM and hipBLASLt (through torch's F.linear, a plain
+    fp16 GEMM + fp16 bias) on every GEMM role of the given configs, same
+    process, same buffers.  One JSON line per role; run it under
+    ``rocprofv3 --kernel-trace --stats`` for the library's kernel names and
+    durations.  hipBLASLt is a yardstick only: it is never on the forward
+    path."""
+    import torch.nn.functional as F
+    from tkmi import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cpu").manual_seed(5)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize()
+        return statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
+
+    for name in configs:
+        cfg = CONFIGS[name]
+        for role, (m, n, k, epi) in gemm_roles(cfg).items():
+            a = (torch.randn(m, k, generator=gen) * 0.5).to(dev, torch.float16)
+            w = (torch.randn(n, k, generator=gen) * k ** -0.5).to(dev, torch.float16)
+            bias = torch.randn(n, generator=gen).to(dev)
+            bias16 = bias.half()
+            out16 = torch.empty(m, n, dtype=torch.float16, device=dev)
+            resid = torch.randn(m, n, generator=gen).to(dev) if epi == "resid" else None
+            out32 = torch.empty_like(resid) if resid is not None else None
+            if epi == "resid":
+                ours = lambda: ops.linear_residual(a, w, bias, resid, out=out32)  # noqa: E731
+            else:
+                ours = lambda: ops.linear(a, w, bias, gelu=epi == "gelu", out=out16)  # noqa: E731
+            plain = lambda: ops.linear(a, w, bias, out=out16)  # noqa: E731
+            lib = lambda: F.linear(a, w, bias16)  # noqa: E731
+            t_lib = timed(lib)
+            t_plain = timed(plain)
+            t_ours = timed(ours)
+            diff = float((plain().float() - lib().float()).abs().max())
+            flop = 2.0 * m * n * k
+            frac = lambda ms: round(flop / (ms * 1e-3) / (PEAK_FP16_TFLOPS * 1e12), 4)  # noqa: E731
+            print(json.dumps({
+                "config": name, "role": role, "m": m, "n": n, "k": k, "epilogue": epi,
+                "hipblaslt_ms": round(t_lib, 5), "tk_plain_ms": round(t_plain, 5), "tk_ms": round(t_ours, 5),
+                "frac_hipblaslt": frac(t_lib), "frac_tk_plain": frac(t_plain), "frac_tk": frac(t_ours),
+                "tk_plain_over_hipblaslt": round(t_plain / t_lib, 3),
+                "max_abs_diff_plain_vs_hipblaslt": diff,
+            }), flush=True)
+            del a, w, bias, bias16, out16, resid, out32
+            torch.cuda.empty_cache()
+    return 0
 
 
 def parse_shape(text: str) -> tuple:
@@ -182,8 +277,8 @@ def cpu_baseline_leg(model, cfg_t, x_host, out_gpu, label: str, mask_host=None):
         xs, sample_b = xs_full[:1], 1
         fn = lambda t: ob.chunked_forward(base, t, q_chunk=2048)  # noqa: E731
         sample = (f"query-chunked fp32 oracle (row-exact to the baseline), sequence 0 of the batch of {b}, "
-                  f"time x{b}; 1 repeat after 0 warmup")
-        reps, warm = 1, 0
+                  f"time x{b}; median of 3 after 1 warmup")
+        reps, warm = 3, 1
     else:
         return None, None
     outs = []
@@ -238,6 +333,9 @@ def main() -> int:
     ap.add_argument("--padding-ratio", type=float, default=0.0,
                     help="prefix padding masks as the harness's --padding-ratio draws them "
                          "(src/torch_transformer_benchmark.py:255-271); 0 = dense")
+    ap.add_argument("--gemm-yardstick", nargs="?", const="C3,C4,C5", default=None,
+                    help="only time this build's GEMMs against hipBLASLt (F.linear) on the GEMM roles of the "
+                         "given configs (default C3,C4,C5); one JSON line per role")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -255,6 +353,12 @@ def main() -> int:
 
     if args.copy_calibration:
         return copy_calibration()
+    if args.gemm_yardstick:
+        names = [c.strip() for c in args.gemm_yardstick.split(",") if c.strip()]
+        bad = [c for c in names if c not in CONFIGS]
+        if bad:
+            raise SystemExit(f"--gemm-yardstick: unknown configs {bad}")
+        return gemm_yardstick(names, max(args.steps, 3))
 
     import tkmi
     from tkmi import ops
@@ -335,28 +439,17 @@ def main() -> int:
     fwd_ms = statistics.median(samples)
     kernels = {}
     for name, ts in per.items():
-        amount, unit, bound = kernel_units(name, cfg_t)
         avg_ms = sum(ts) / len(ts)
-        rate = amount / (avg_ms * 1e-3)
-        if bound == "mfma":
-            ach, peak, u = rate / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s"
-        else:
-            ach, peak, u = rate / 1e9, PEAK_HBM_GBPS, "GB/s"
         kernels[name] = {
             "avg_ms": round(avg_ms, 5),
             "launches_per_step": len(ts) // args.steps,
             "ms_per_step": round(sum(ts) / args.steps, 5),
-            "bound": bound,
-            "achieved": round(ach, 2),
-            "unit": u,
-            "frac": round(ach / peak, 4),
-            "algorithmic_per_launch": amount,
-            "algorithmic_unit": unit,
+            **kernel_roofline(name, cfg_t, avg_ms),
         }
-        if bound == "hbm":
+        if kernels[name]["bound"] == "hbm":
             # a launch whose bytes fit the 256 MB Infinity Cache may be served from it
             # (the steps re-run the same buffers), so its GB/s is not an HBM figure
-            kernels[name]["cache_resident"] = amount <= INFINITY_CACHE_BYTES
+            kernels[name]["cache_resident"] = kernels[name]["algorithmic_per_launch"] <= INFINITY_CACHE_BYTES
     dom_name = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     dom = kernels[dom_name]
     roofline = {
@@ -366,6 +459,8 @@ def main() -> int:
         "peak": PEAK_FP16_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBPS,
         "unit": dom["unit"],
         "frac": dom["frac"],
+        "frac_mfma": dom.get("frac_mfma"),
+        "frac_hbm": dom.get("frac_hbm"),
         "traffic": measured_traffic(workload, dom_name) if args.dtype == "float32" else None,
     }
     if roofline["traffic"] is not None:

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TKMI_ABI_VERSION 2
+#define TKMI_ABI_VERSION 3
 
 typedef uint16_t tk_half;
 
@@ -81,15 +81,18 @@ int tk_ln_cast(const float *x, const float *w, const float *b, void *out,
 
 /*
  * Residual add + LayerNorm + cast.
- *   s = x + y (fp32);  h = LN(s) cast to h_dtype.
- * y has y_dtype (TK_F16 or TK_F32).  sum_out may be NULL (s not stored) and
- * may alias x.  cols in [1, 8192].
+ *   s = x + y (added in fp32);  h = LN(s) (statistics of the fp32 sum) cast
+ *   to h_dtype;  s stored in x's dtype.
+ * x has x_dtype and y has y_dtype (TK_F16 or TK_F32 each); sum_out, when not
+ * NULL, is [rows, cols] of x_dtype and may alias x (NULL: s not stored).
+ * cols in [1, 8192].
  * Replaces fused_kernels.add_ln_fwd / _add_ln_kernel
- * (src/fused_kernels.py:196-238, :114-161).
+ * (src/fused_kernels.py:196-238, :114-161; s = empty_like(x) at :216).
  */
-int tk_add_ln_cast(const float *x, const void *y, int y_dtype, const float *w,
-                   const float *b, float *sum_out, void *h_out, int h_dtype,
-                   int64_t rows, int64_t cols, float eps, void *stream);
+int tk_add_ln_cast(const void *x, int x_dtype, const void *y, int y_dtype,
+                   const float *w, const float *b, void *sum_out, void *h_out,
+                   int h_dtype, int64_t rows, int64_t cols, float eps,
+                   void *stream);
 
 /*
  * GEMM  C[m, n] = epilogue( sum_k A[m, k] * W[n, k] + bias[n] )

@@ -23,6 +23,43 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: long-running parity case (full-size configs)")
 
 
+# Worst parity margin per benchmark config over every checked trial:
+# config -> {"max_abs", "budget_frac", "trials"}.  budget_frac is the largest
+# |d| / max(atol, rtol * |ref|) over the elements (1.0 = on the harness's
+# limit, src/torch_transformer_benchmark.py:309-316); the terminal summary
+# prints it so the GPU run's log carries the margins, not only a pass count.
+PARITY_MARGINS = {}
+
+
+def budget_fraction(ref, got, atol=0.002, rtol=0.02):
+    """Largest share of the per-element tolerance used (inf if anything is non-finite)."""
+    ref = ref.detach().float().cpu()
+    got = got.detach().float().cpu()
+    if not (torch.isfinite(ref).all() and torch.isfinite(got).all()):
+        return float("inf")
+    lim = torch.clamp(ref.abs() * rtol, min=atol)
+    return float(((got - ref).abs() / lim).max()) if ref.numel() else 0.0
+
+
+def record_parity(config: str, ref, got, max_abs: float) -> None:
+    frac = budget_fraction(ref, got)
+    cur = PARITY_MARGINS.setdefault(config, {"max_abs": 0.0, "budget_frac": 0.0, "trials": 0})
+    cur["max_abs"] = max(cur["max_abs"], float(max_abs))
+    cur["budget_frac"] = max(cur["budget_frac"], frac)
+    cur["trials"] += 1
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    if not PARITY_MARGINS:
+        return
+    tr = terminalreporter
+    tr.write_line("parity margins (worst over the checked trials; budget |d| <= 0.002 or <= 0.02*|ref|):")
+    for name in sorted(PARITY_MARGINS):
+        m = PARITY_MARGINS[name]
+        tr.write_line(f"  {name}: max|d| {m['max_abs']:.3e}, {100.0 * m['budget_frac']:.1f}% of the "
+                      f"element budget, {m['trials']} trials")
+
+
 def pytest_collection_modifyitems(config, items):
     if torch.cuda.is_available():
         return

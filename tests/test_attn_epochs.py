@@ -296,7 +296,10 @@ def test_key_masked_loop_adds_only_the_mask_work():
     assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "s_waitcnt vmcnt(4)", "v_cmp_",
                              "s_mov_b32 s9", "s_mov_b64 s[94:95]", "s_bfe_i32", "v_cndmask_b32",
                              "v_mov_b32 v196, 0xff800000")) for l in extra), extra[:5]
-    assert sum(1 for l in masked if l.startswith("v_cndmask_b32")) == 4 * (32 + 2)
+    # per epoch: 32 score selects and the m = -inf guard's 2 (masked only), and the
+    # rescale's alpha = 1 select for m_new = -inf (both loops)
+    assert sum(1 for l in dense if l.startswith("v_cndmask_b32")) == 4
+    assert sum(1 for l in masked if l.startswith("v_cndmask_b32")) == 4 * (32 + 2 + 1)
     it = iter(masked)  # the dense loop is a subsequence of the masked one, in order
     assert all(any(m == l for m in it) for l in dense)
     src = (CSRC / "tk_attention.hip").read_text()

@@ -23,8 +23,13 @@ Epoch e of the pair body (key tile e = keys 64e .. 64e+63) does, for every wave:
 Each lane performs the same operations on the same operands in the same order as the compiled
 epoch, so the results are bit-identical to it.  The loop covers the epochs [1, 1 + 4*groups),
 which the host side chooses so that no key tile in them needs a causal or length mask (every key
-is below every query row of the workgroup) and no copy is clamped to the last tile; m_run is
-finite there (epoch 0 saw key 0), so the -inf guards of the compiled epoch are not needed.
+is below every query row of the workgroup) and no copy is clamped to the last tile.  Without a
+key mask m_run is finite there (epoch 0 saw key 0).  With one, every row of the workgroup has
+seen the same keys with the same validity (no causal mask applies in these epochs), so m_run and
+m_tile are -inf for all rows of a wave or for none: the wave-wide rescale test never fires for a
+row whose m_new would be -inf.  The rescale still maps m_new = -inf to alpha = 1 (one compare and
+one select on that rare path), so l and O cannot turn into NaN if the loop's gate ever admits
+rows with different key histories.
 
 One loop iteration is 4 epochs, so epoch e = 1 + 4i + u (loop position u) reads V(e-1) from
 V slot (e-1) % 4 = u and writes V(e+1) into slot (u + 2) % 4: both are immediate LDS offsets.
@@ -178,7 +183,9 @@ def epoch(u: int, kmask: bool = False) -> list[str]:
     L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",               # m_new
           f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
           f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
-          f"v_mov_b32 {v(MR)}, {v(TMP)}", "s_nop 0",
+          f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",              # m_new = -inf: alpha = 1
+          f"v_mov_b32 {v(MR)}, {v(TMP)}",
+          f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
           f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
           "s_mov_b32 %[flag], 1"]
     L += [f"L_norescale_{u}_%=:"]

@@ -25,7 +25,13 @@ Each lane performs the compiled step's operations on the same operands in the sa
 MFMA accumulation chains, the exponentials, the fp16 packing and the row-sum order; the row max
 is exact in any order), so the results are bit-identical to it.  The loop runs steps
 [1, 1 + 2*groups), which the host side chooses so that no key tile in them needs a mask and
-every copy is a whole tile; m_run is finite there.  Two steps per iteration: the score, P and
+every copy is a whole tile.  Without a key mask m_run is finite there (step 0 saw key 0); with
+one, every row of the workgroup has seen the same keys with the same validity (no causal mask
+applies in these steps), so m_run and m_tile are -inf for all rows of a wave or for none and the
+wave-wide rescale test never fires for a row whose m_new would be -inf.  The rescale still maps
+m_new = -inf to alpha = 1 (one compare and one select on that rare path), so l and O cannot turn
+into NaN if the loop's gate ever admits rows with different key histories.  Two steps per
+iteration: the score, P and
 max registers swap roles between them (the compiled loop's s_a/s_b, pf_a/pf_b, mx_a/mx_b), the
 K slot (2 slots) follows the parity and the V slots (3) rotate through SGPR trackers.
 
@@ -113,7 +119,9 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
     L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",                # m_new
           f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
           f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
-          f"v_mov_b32 {v(MR)}, {v(TMP)}", "s_nop 0",
+          f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",               # m_new = -inf: alpha = 1
+          f"v_mov_b32 {v(MR)}, {v(TMP)}",
+          f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
           f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
           "s_mov_b32 %[flag], 1"]
     L += [f"L_norescale_{par}_%=:"]

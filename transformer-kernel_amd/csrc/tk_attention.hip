@@ -403,12 +403,14 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   for (int e = 0; e < 32; ++e) mx_a = fmaxf(mx_a, s_a[e >> 4][e & 15]);
   __syncthreads();  // K(0) read by every wave before step 0 refills its slot
 
-  // ---- hand-ordered steady state (head_dim 64, 4 or 8 waves, causal, no key mask) ----
+  // ---- hand-ordered steady state (head_dim 64, 4 or 8 waves, causal; dense or key-masked) ----
   // Steps [1, 1 + 2*groups) run from an asm loop (tk_attn_steps64{,_w8}.inc, made by
   // gen_attn_steps64.py) that keeps each step's 32 exponentials between its 16
   // MFMAs; every lane does the compiled step's arithmetic in the same order, so
   // the results are bit-identical.  Those steps' key tiles lie below the query
-  // block (no mask) and their copies are whole tiles (K tile kt+2 < S/kBN); the
+  // block (no causal mask; a key mask is applied by the _kmask loops, which
+  // set invalid keys' scores to -inf) and their copies are whole tiles (K tile
+  // kt+2 < S/kBN); the
   // copies use 32-bit offsets from the K and V bases (span check) and the K read
   // addresses are formed by XOR on bits 5-6 of a 256-byte-aligned row offset.
   int groups = 0;
@@ -416,7 +418,9 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     const int last = min(q0 / kBN - 1, min(n_kt, p.S / kBN) - 3);
     const int64_t span =
         ((int64_t)n_kt + 2) * max(k_tile, v_tile) * 2 + (int64_t)kBN * max(p.ks[2], p.vs[2]) * 2;
-    if (last >= 2 && span < (1ll << 31) && (lds_base & 255) == 0) groups = last / 2;
+    // 32-bit unsigned offsets: only for non-negative row strides
+    if (last >= 2 && p.ks[2] >= 0 && p.vs[2] >= 0 && span < (1ll << 31) && (lds_base & 255) == 0)
+      groups = last / 2;
   }
 
   const BoolC<true> T{};
@@ -1417,7 +1421,9 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
     const int e_lim = min(q0 / kBN, min(n_kt, p.S / kBN) - 2);
     const int64_t span =
         ((int64_t)n_kt + 2) * max(k_tile, v_tile) * 2 + (int64_t)kBN * max(p.ks[2], p.vs[2]) * 2;
-    if (e_lim > 1 && span < (1ll << 31) && (lds_base & 255) == 0) groups = (e_lim - 1) / 4;
+    // 32-bit unsigned offsets: only for non-negative row strides
+    if (e_lim > 1 && p.ks[2] >= 0 && p.vs[2] >= 0 && span < (1ll << 31) && (lds_base & 255) == 0)
+      groups = (e_lim - 1) / 4;
   }
   // Pinned: O^T v[64:127], Q v[128:159], P region A v[160:175] (P(0) in, P(4*groups)
   // out), m_run v192, l_run v193; the loop's other registers are clobbered.

@@ -62,19 +62,21 @@ struct Vec<f16, NT> {
   static __device__ __forceinline__ void store1(f16* p, float v) { *p = (f16)v; }
 };
 
-// HAS_Y: s = x + y (residual add) else s = x.  row_valid (nullable): an
+// HAS_Y: s = x + y (residual add, in fp32) else s = x.  The sum is stored in
+// x's type XT (src/fused_kernels.py:216,143-147: s = x + y in x's dtype); the
+// statistics use the fp32 sum before that rounding.  row_valid (nullable): an
 // invalid row's normalised output is written as zeros.
-template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT, bool NT>
+template <int LPR, int NV, int VW, bool HAS_Y, typename XT, typename YT, typename OT, bool NT>
 __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
-    const float* x, const YT* __restrict__ y, const float* __restrict__ w,
-    const float* __restrict__ b, float* sum_out, OT* __restrict__ out, int64_t rows,
+    const XT* x, const YT* __restrict__ y, const float* __restrict__ w,
+    const float* __restrict__ b, XT* sum_out, OT* __restrict__ out, int64_t rows,
     int cols, float eps, const uint8_t* __restrict__ row_valid) {
   constexpr int kRowsPerBlock = kBlock / LPR;
   const int lane = threadIdx.x % LPR;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
   if (row >= rows) return;
 
-  const float* xr = x + row * cols;
+  const XT* xr = x + row * cols;
   float s[NV * VW];
 
 #pragma unroll
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
     const int c0 = (v * LPR + lane) * VW;
     if constexpr (VW == 4) {
       if (c0 < cols) {
-        Vec<float, NT>::load4(xr + c0, &s[v * 4]);
+        Vec<XT, NT>::load4(xr + c0, &s[v * 4]);
         if constexpr (HAS_Y) {
           float t[4];
           Vec<YT, NT>::load4(y + row * cols + c0, t);
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
       }
     } else {
       if (c0 < cols) {
-        s[v] = xr[c0];
+        s[v] = Vec<XT>::load1(xr + c0);
         if constexpr (HAS_Y) s[v] += Vec<YT>::load1(y + row * cols + c0);
       } else {
         s[v] = 0.f;
@@ -104,13 +106,13 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
   }
 
   if (HAS_Y && sum_out != nullptr) {
-    float* sr = sum_out + row * cols;
+    XT* sr = sum_out + row * cols;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int c0 = (v * LPR + lane) * VW;
       if (c0 < cols) {
-        if constexpr (VW == 4) Vec<float, NT>::store4(sr + c0, &s[v * 4]);
-        else sr[c0] = s[v];
+        if constexpr (VW == 4) Vec<XT, NT>::store4(sr + c0, &s[v * 4]);
+        else Vec<XT>::store1(sr + c0, s[v]);
       }
     }
   }
@@ -158,31 +160,31 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(
 
 constexpr int64_t kStreamBytes = 128ll << 20;  // fp32 input size from which the accesses are non-temporal
 
-template <int LPR, int NV, int VW, bool HAS_Y, typename YT, typename OT>
-int launch_rows(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
+template <int LPR, int NV, int VW, bool HAS_Y, typename XT, typename YT, typename OT>
+int launch_rows(const XT* x, const YT* y, const float* w, const float* b, XT* sum_out,
                 OT* out, int64_t rows, int cols, float eps, const uint8_t* row_valid, hipStream_t st) {
   constexpr int kRowsPerBlock = kBlock / LPR;
   const int64_t grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (VW == 4 && rows * cols * 4 >= kStreamBytes)
-    hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, YT, OT, true>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, XT, YT, OT, true>), dim3((unsigned)grid),
                        dim3(kBlock), 0, st, x, y, w, b, sum_out, out, rows, cols, eps, row_valid);
   else
-    hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, YT, OT, false>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, VW, HAS_Y, XT, YT, OT, false>), dim3((unsigned)grid),
                        dim3(kBlock), 0, st, x, y, w, b, sum_out, out, rows, cols, eps, row_valid);
   return check_launch("layernorm");
 }
 
 // Picks lanes-per-row and register-vector count for `cols`.
-template <bool HAS_Y, typename YT, typename OT>
-int dispatch(const float* x, const YT* y, const float* w, const float* b, float* sum_out,
+template <bool HAS_Y, typename XT, typename YT, typename OT>
+int dispatch(const XT* x, const YT* y, const float* w, const float* b, XT* sum_out,
              OT* out, int64_t rows, int cols, float eps, const uint8_t* row_valid, hipStream_t st) {
 #define TK_LN(LPR, NV, VW) \
-  return launch_rows<LPR, NV, VW, HAS_Y, YT, OT>(x, y, w, b, sum_out, out, rows, cols, eps, row_valid, st)
-  // 16-byte vector path needs cols % 4 == 0 and 16-byte aligned fp32 rows
-  // (8-byte for fp16 rows); anything else takes the scalar path.
+  return launch_rows<LPR, NV, VW, HAS_Y, XT, YT, OT>(x, y, w, b, sum_out, out, rows, cols, eps, row_valid, st)
+  // 4-wide vector path needs cols % 4 == 0 and rows aligned to 4 elements
+  // (16 bytes for fp32 rows, 8 for fp16); anything else takes the scalar path.
   auto al = [](const void* p, uintptr_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; };
-  const bool vec_ok = cols % 4 == 0 && al(x, 16) && al(w, 16) && al(b, 16) && al(sum_out, 16) &&
-                      al(y, sizeof(YT) * 4) && al(out, sizeof(OT) * 4);
+  const bool vec_ok = cols % 4 == 0 && al(x, sizeof(XT) * 4) && al(w, 16) && al(b, 16) &&
+                      al(sum_out, sizeof(XT) * 4) && al(y, sizeof(YT) * 4) && al(out, sizeof(OT) * 4);
   if (vec_ok) {
     if (cols <= 64) TK_LN(16, 1, 4);
     if (cols <= 128) TK_LN(32, 1, 4);
@@ -228,29 +230,43 @@ extern "C" int tk_ln_cast(const float* x, const float* w, const float* b, void* 
   hipStream_t st = as_stream(stream);
   const int c = (int)cols;
   if (out_dtype == TK_F16)
-    return dispatch<false, float, f16>(x, nullptr, w, b, nullptr, (f16*)out, rows, c, eps, row_valid, st);
-  return dispatch<false, float, float>(x, nullptr, w, b, nullptr, (float*)out, rows, c, eps, row_valid, st);
+    return dispatch<false, float, float, f16>(x, nullptr, w, b, nullptr, (f16*)out, rows, c, eps, row_valid, st);
+  return dispatch<false, float, float, float>(x, nullptr, w, b, nullptr, (float*)out, rows, c, eps, row_valid,
+                                              st);
 }
 
-extern "C" int tk_add_ln_cast(const float* x, const void* y, int y_dtype, const float* w,
-                              const float* b, float* sum_out, void* h_out, int h_dtype,
+namespace {
+template <typename XT>
+int add_ln_x(const XT* x, const void* y, int y_dtype, const float* w, const float* b, XT* sum_out,
+             void* h_out, int h_dtype, int64_t rows, int c, float eps, hipStream_t st) {
+  if (y_dtype == TK_F16) {
+    if (h_dtype == TK_F16)
+      return dispatch<true, XT, f16, f16>(x, (const f16*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr, st);
+    return dispatch<true, XT, f16, float>(x, (const f16*)y, w, b, sum_out, (float*)h_out, rows, c, eps, nullptr,
+                                          st);
+  }
+  if (h_dtype == TK_F16)
+    return dispatch<true, XT, float, f16>(x, (const float*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr,
+                                          st);
+  return dispatch<true, XT, float, float>(x, (const float*)y, w, b, sum_out, (float*)h_out, rows, c, eps,
+                                          nullptr, st);
+}
+}  // namespace
+
+extern "C" int tk_add_ln_cast(const void* x, int x_dtype, const void* y, int y_dtype, const float* w,
+                              const float* b, void* sum_out, void* h_out, int h_dtype,
                               int64_t rows, int64_t cols, float eps, void* stream) {
   TK_REQUIRE(x && y && w && b && h_out, TK_ERR_ARG, "tk_add_ln_cast: null pointer");
   TK_REQUIRE(rows >= 0 && cols >= 1 && cols <= kMaxCols, TK_ERR_ARG,
              "tk_add_ln_cast: rows=%lld cols=%lld outside [0, inf) x [1, %lld]",
              (long long)rows, (long long)cols, (long long)kMaxCols);
-  TK_REQUIRE((y_dtype == TK_F16 || y_dtype == TK_F32) && (h_dtype == TK_F16 || h_dtype == TK_F32),
-             TK_ERR_ARG, "tk_add_ln_cast: bad dtype (y=%d, h=%d)", y_dtype, h_dtype);
+  TK_REQUIRE((x_dtype == TK_F16 || x_dtype == TK_F32) && (y_dtype == TK_F16 || y_dtype == TK_F32) &&
+                 (h_dtype == TK_F16 || h_dtype == TK_F32),
+             TK_ERR_ARG, "tk_add_ln_cast: bad dtype (x=%d, y=%d, h=%d)", x_dtype, y_dtype, h_dtype);
   if (rows == 0) return TK_OK;
   hipStream_t st = as_stream(stream);
   const int c = (int)cols;
-  if (y_dtype == TK_F16) {
-    if (h_dtype == TK_F16)
-      return dispatch<true, f16, f16>(x, (const f16*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr, st);
-    return dispatch<true, f16, float>(x, (const f16*)y, w, b, sum_out, (float*)h_out, rows, c, eps, nullptr, st);
-  }
-  if (h_dtype == TK_F16)
-    return dispatch<true, float, f16>(x, (const float*)y, w, b, sum_out, (f16*)h_out, rows, c, eps, nullptr, st);
-  return dispatch<true, float, float>(x, (const float*)y, w, b, sum_out, (float*)h_out, rows, c, eps, nullptr,
-                                      st);
+  if (x_dtype == TK_F16)
+    return add_ln_x<f16>((const f16*)x, y, y_dtype, w, b, (f16*)sum_out, h_out, h_dtype, rows, c, eps, st);
+  return add_ln_x<float>((const float*)x, y, y_dtype, w, b, (float*)sum_out, h_out, h_dtype, rows, c, eps, st);
 }

@@ -13,7 +13,7 @@ import threading
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_void_p
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtkmi.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TK_OK, TK_ERR_ARG, TK_ERR_UNSUPPORTED, TK_ERR_HIP = 0, -1, -2, -3
 TK_F32, TK_F16 = 0, 1
@@ -31,7 +31,8 @@ SIGNATURES = {
     ),
     "tk_add_ln_cast": (
         c_int,
-        [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float, c_void_p],
+        [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float,
+         c_void_p],
     ),
     "tk_gemm": (
         c_int,

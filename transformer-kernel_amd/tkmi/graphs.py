@@ -1,26 +1,32 @@
-"""Whole-forward HIP-graph capture of ``OptimizedTransformer``.
+"""Whole-forward HIP-graph replay of ``OptimizedTransformer``.
 
-Counterpart of the reference's ``GraphedTransformer`` (src/cuda_graphs.py:61-164):
+Behaviour (the reference's ``GraphedTransformer``, src/cuda_graphs.py:61-164):
 
-* the first ``WARMUP_BEFORE_CAPTURE`` calls per (shape, dtype, device) run
-  eagerly (the harness's accuracy trials use fresh inputs; capture lands in
-  its warm-up phase on the fixed timing input);
-* capture records the dense forward into a ``torch.cuda.CUDAGraph`` (a HIP
-  graph on ROCm) after two warm-up calls on a side stream;
-* a replay with a different input tensor of the same shape first copies it
-  into the captured input buffer (one device-to-device copy);
-* a padded (non-dense) mask always takes the eager path;
-* any capture failure prints one warning and leaves the model eager for the
-  rest of the process.
+* each (input shape, dtype, device) runs eagerly for its first
+  ``WARMUP_BEFORE_CAPTURE`` dense calls, so the harness's accuracy trials
+  (fresh inputs) stay eager and the capture lands on its fixed timing input;
+* the next dense call records one forward into a ``torch.cuda.CUDAGraph``
+  (a HIP graph on ROCm) following torch's documented capture recipe: warm-up
+  forwards on a side stream that waits for the current one, the current
+  stream waiting for them, then capture under ``torch.cuda.graph``;
+* later calls replay it; an input that is not the captured allocation is
+  first copied into it (one device-to-device copy), and the captured output
+  tensor is returned;
+* a padded (non-dense) mask, a CPU input, or a process in which a capture
+  has failed (one warning) run the eager forward;
+* moving the module (``_apply``) or changing any parameter drops the
+  recorded graphs: they hold pointers to the packed weights they were
+  captured with.
 
-The replayed work is exactly the eager kernel sequence (the same HIP
-kernels, same arguments), so numerics are identical.  None of the kernels
-issues a memset, and all scratch buffers are allocated from the graph's
-private memory pool during capture.
+A replay launches exactly the eager kernel sequence with the same
+arguments, so its output is bit-identical to the eager forward's.  None of
+the kernels issues a memset, and every intermediate buffer is allocated from
+the graph's private pool during capture.
 """
 
 from __future__ import annotations
 
+import dataclasses
 import warnings
 from typing import Dict, Optional, Tuple
 
@@ -30,17 +36,19 @@ from .model import OptimizedTransformer
 
 __all__ = ["GraphedTransformer", "WARMUP_BEFORE_CAPTURE"]
 
-WARMUP_BEFORE_CAPTURE = 8
+WARMUP_BEFORE_CAPTURE = 8  # eager dense calls per input signature before the capture
+_CAPTURE_WARMUPS = 2       # side-stream forwards ahead of the capture
+
+_Signature = Tuple[Tuple[int, ...], torch.dtype, torch.device]
 
 
-class _GraphState:
-    __slots__ = ("eager_calls", "graph", "static_x", "static_out")
+@dataclasses.dataclass(frozen=True)
+class _Replay:
+    """A recorded forward: the graph and the allocations it reads and writes."""
 
-    def __init__(self) -> None:
-        self.eager_calls = 0
-        self.graph: Optional[torch.cuda.CUDAGraph] = None
-        self.static_x: Optional[torch.Tensor] = None
-        self.static_out: Optional[torch.Tensor] = None
+    graph: "torch.cuda.CUDAGraph"
+    x_in: torch.Tensor
+    y_out: torch.Tensor
 
 
 class GraphedTransformer(OptimizedTransformer):
@@ -48,50 +56,61 @@ class GraphedTransformer(OptimizedTransformer):
 
     def __init__(self, config, settings=None) -> None:
         super().__init__(config, settings)
-        self._graphs: Dict[Tuple, _GraphState] = {}
-        self._capture_failed = False
+        self._eager_calls: Dict[_Signature, int] = {}
+        self._replays: Dict[_Signature, _Replay] = {}
+        self._replay_weights: Optional[tuple] = None  # weight-cache key the replays were recorded with
+        self._no_graphs = False
+
+    def _forget_replays(self) -> None:
+        self._eager_calls.clear()
+        self._replays.clear()
 
     def _apply(self, *args, **kwargs):
         result = super()._apply(*args, **kwargs)
-        self._graphs = {}  # captured graphs hold pointers to the old weights
+        self._forget_replays()
+        self._no_graphs = False  # another device may capture where this one failed
         return result
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if self._capture_failed or not x.is_cuda or not self._mask_is_dense(valid_token_mask):
+        if self._no_graphs or not x.is_cuda or not self._mask_is_dense(valid_token_mask):
             return super().forward(x, valid_token_mask)
-        # The packed-weight cache must be current before capture or replay;
-        # a parameter update (version bump) invalidates the captured graphs.
-        key_before = self._weight_cache_key
-        self._weights()
-        if self._weight_cache_key != key_before:
-            self._graphs = {}
-        key = (tuple(x.shape), x.dtype, x.device)
-        state = self._graphs.setdefault(key, _GraphState())
-        if state.graph is None:
-            state.eager_calls += 1
-            if state.eager_calls <= WARMUP_BEFORE_CAPTURE:
+        self._weights()  # bring the packed weights up to date before any replay
+        if self._weight_cache_key != self._replay_weights:
+            self._forget_replays()
+            self._replay_weights = self._weight_cache_key
+        sig = (tuple(x.shape), x.dtype, x.device)
+        rec = self._replays.get(sig)
+        if rec is None:
+            calls = self._eager_calls.get(sig, 0) + 1
+            self._eager_calls[sig] = calls
+            if calls <= WARMUP_BEFORE_CAPTURE:
+                return super().forward(x, None)  # dense: the mask carries nothing
+            rec = self._record(x)
+            if rec is None:
                 return super().forward(x, None)
-            self._capture(state, x)
-            if state.graph is None:
-                return super().forward(x, None)
-        if x.data_ptr() != state.static_x.data_ptr():
-            state.static_x.copy_(x)
-        state.graph.replay()
-        return state.static_out
+            self._replays[sig] = rec
+        if x.data_ptr() != rec.x_in.data_ptr():
+            rec.x_in.copy_(x)
+        rec.graph.replay()
+        return rec.y_out
 
-    def _capture(self, state: _GraphState, x: torch.Tensor) -> None:
+    def _record(self, x: torch.Tensor) -> Optional[_Replay]:
+        """Capture one dense forward reading ``x``'s allocation (kept alive by the record)."""
+        eager = OptimizedTransformer.forward
         try:
-            static_x = x  # replays read this allocation; keep it alive
+            main = torch.cuda.current_stream(x.device)
             side = torch.cuda.Stream(device=x.device)
-            side.wait_stream(torch.cuda.current_stream(x.device))
+            side.wait_stream(main)
             with torch.cuda.stream(side):
-                for _ in range(2):
-                    OptimizedTransformer.forward(self, static_x, None)
-            torch.cuda.current_stream(x.device).wait_stream(side)
+                for _ in range(_CAPTURE_WARMUPS):
+                    eager(self, x, None)
+            main.wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                static_out = OptimizedTransformer.forward(self, static_x, None)
-            state.graph, state.static_x, state.static_out = graph, static_x, static_out
+                y = eager(self, x, None)
         except Exception as exc:  # pragma: no cover - depends on the runtime
-            self._capture_failed = True
-            warnings.warn(f"HIP graph capture failed ({exc!r}); staying eager")
+            self._no_graphs = True
+            self._forget_replays()
+            warnings.warn(f"HIP graph capture failed ({exc!r}); this model stays eager")
+            return None
+        return _Replay(graph, x, y)

@@ -124,10 +124,13 @@ def ln_fwd(x, weight, bias, eps: float, out_dtype: Optional[torch.dtype] = None,
 
 def add_ln_fwd(x, y, weight, bias, eps: float, out_dtype: Optional[torch.dtype] = None,
                write_sum: bool = True):
-    """Residual add + LayerNorm: returns ``(s, h)``, s = x + y in fp32, h = LN(s).
+    """Residual add + LayerNorm: returns ``(s, h)``, h = LN(s).
 
-    With ``write_sum=False`` the sum is not stored and ``s`` is None (the
-    final norm of the model, src/optimized.py:542-553).
+    As src/fused_kernels.py:196-238: ``s = x + y`` is added in fp32 and
+    returned in ``x``'s dtype (float32 or float16); the statistics use the
+    fp32 sum; ``h`` is in ``out_dtype`` (default ``x.dtype``).  With
+    ``write_sum=False`` the sum is not stored and ``s`` is None (the final
+    norm of the model, src/optimized.py:542-553).
     """
     _require_cuda(x, y, weight, bias)
     if x.shape != y.shape:
@@ -135,14 +138,14 @@ def add_ln_fwd(x, y, weight, bias, eps: float, out_dtype: Optional[torch.dtype] 
     out_dtype = x.dtype if out_dtype is None else out_dtype
     shape = x.shape
     cols = shape[-1]
-    x2 = x.float().contiguous().view(-1, cols)
+    x2 = x.contiguous().view(-1, cols)
     y2 = y.contiguous().view(-1, cols)
     w = weight.float().contiguous()
     b = bias.float().contiguous()
     s = torch.empty_like(x2) if write_sum else None
     h = torch.empty(x2.shape, dtype=out_dtype, device=x.device)
     _launch(
-        "add_ln_cast", "tk_add_ln_cast", x2.data_ptr(), y2.data_ptr(), _code(y2.dtype),
+        "add_ln_cast", "tk_add_ln_cast", x2.data_ptr(), _code(x2.dtype), y2.data_ptr(), _code(y2.dtype),
         w.data_ptr(), b.data_ptr(), s.data_ptr() if s is not None else None, h.data_ptr(),
         _code(out_dtype), x2.shape[0], cols, float(eps), _stream(x),
     )
