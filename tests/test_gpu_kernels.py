@@ -114,6 +114,30 @@ def test_layernorm_script_matrix(n_cols):
             assert fp16_excess(h, h_want, atol) <= 0
 
 
+@pytest.mark.parametrize("cols", [64, 100, 1024])
+@pytest.mark.parametrize("y_dtype", [torch.float16, torch.float32])
+def test_add_ln_half_x_returns_sum_in_x_dtype(cols, y_dtype):
+    """fp16 x: s = x + y is added in fp32 and returned in x's dtype, h = LN of the
+    fp32 sum in out_dtype (default x's dtype), as src/fused_kernels.py:196-238
+    (s = empty_like(x2) at :216, the sum stored through sum_ptr's element type at
+    :143-147, the statistics from the fp32 s at :149-154).  cols 100 takes the
+    scalar path."""
+    rows = 129
+    x = seeded(rows, cols, dtype=torch.float16, seed=cols + 40) * 2
+    y = seeded(rows, cols, dtype=y_dtype, seed=cols + 41)
+    w, b = seeded(cols, seed=cols + 42, scale=0.5) + 1.0, seeded(cols, seed=cols + 43, scale=0.5)
+    xg, yg, wg, bg = x.to(DEV), y.to(DEV), w.to(DEV), b.to(DEV)
+    sum32 = x.float() + y.float()
+    s, h = ops.add_ln_fwd(xg, yg, wg, bg, 1e-5)
+    assert s.dtype == torch.float16 and h.dtype == torch.float16 and s.shape == x.shape
+    assert torch.equal(s.cpu(), sum32.half())  # one fp32 add, one rounding: bit-exact
+    assert fp16_excess(h, ob.layer_norm_ref(sum32, w, b, 1e-5, torch.float16), 1e-3) <= 0
+    s2, h32 = ops.add_ln_fwd(xg, yg, wg, bg, 1e-5, torch.float32)
+    assert s2.dtype == torch.float16 and torch.equal(s2.cpu(), s.cpu())
+    # the statistics come from the fp32 sum, not from its fp16 rounding
+    torch.testing.assert_close(h32.cpu(), ob.layer_norm_ref(sum32, w, b, 1e-5), atol=1e-5, rtol=1e-5)
+
+
 @pytest.mark.parametrize("cols", [512, 2048, 4096, 8192])
 def test_layernorm_model_widths_no_sum(cols):
     rows = 300
@@ -175,6 +199,30 @@ def test_gemm_residual_inplace(m, n, k):
     assert out.data_ptr() == rg.data_ptr()
     # fp32 output: accumulation-order differences only
     torch.testing.assert_close(out.cpu(), resid + ref, atol=5e-5, rtol=1e-5)
+
+
+# 256 x 256 tiles: launches of whole tiles (M, N multiples of 256, K of 128) run
+# the ping-pong K loop, others the two-stage loop (or 128 x 128 tiles); per
+# output element both accumulate the same MFMA k-steps in the same order, so
+# the first M rows of an (M + 8)-row launch equal the whole-tile launch bit for bit.
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 2048), (8192, 8192, 512), (8192, 2048, 4096)])
+@pytest.mark.parametrize("epi", ["bias", "gelu", "resid"])
+def test_gemm_pingpong_matches_two_stage_loop(m, n, k, epi):
+    a, w, bias, ref = _gemm_inputs(m + 8, n, k, seed=31)
+    ag, wg, bg = a.to(DEV), w.to(DEV), bias.to(DEV)
+    if epi == "resid":
+        resid = seeded(m + 8, n, seed=32).to(DEV)
+        whole = ops.linear_residual(ag[:m], wg, bg, resid[:m].contiguous())
+        ragged = ops.linear_residual(ag, wg, bg, resid)
+        want = resid.cpu() + ref
+        tol = dict(atol=5e-5, rtol=1e-5)
+    else:
+        whole = ops.linear(ag[:m], wg, bg, gelu=epi == "gelu")
+        ragged = ops.linear(ag, wg, bg, gelu=epi == "gelu")
+        want = (ob.gelu_ref(ref) if epi == "gelu" else ref).half().float()
+        tol = dict(atol=1e-3, rtol=1e-3)
+    assert torch.equal(whole, ragged[:m])
+    torch.testing.assert_close(ragged.cpu().float(), want, **tol)
 
 
 @pytest.mark.parametrize("mode", ["keep", "zero"])

@@ -19,7 +19,10 @@
 // the copies are bank-conflict free on gfx950's 64-bank LDS.  Block ids are
 // remapped so that the tiles of one XCD (workgroups are dealt round-robin
 // over the 8 XCDs) form a compact group of output tiles sharing A rows and
-// W rows in that XCD's L2.
+// W rows in that XCD's L2.  Whole 256x256 tiles (M, N multiples of 256, K of
+// 128) run the ping-pong K loop instead (Mainloop::run_pingpong): the two
+// waves of each SIMD alternate between a phase of LDS reads and copies and a
+// phase of MFMAs only, so one of them always feeds the matrix core.
 #include "tk_attn_tile.hpp"
 
 namespace tk {
@@ -27,6 +30,7 @@ namespace {
 
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const f16x8 lds_f16x8;
 
 struct GemmArgs {
   const f16* a;
@@ -82,6 +86,48 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// Raw buffer resource for buffer_load ... lds: base address, no stride, no
+// range limit (the callers copy whole tiles only), gfx9 data format word.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 raw_buffer_rsrc(const void* base) {
+  const uint64_t b = (uint64_t)base;
+  return i32x4{(int32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
+               (int32_t)(__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu), -1, 0x00020000};
+}
+
+// One wave's 1 KB global -> LDS copy (buffer_load_dwordx4 ... lds: lane l's
+// 16 bytes from rsrc + soff + voff land at lds_addr + 16 l).  Issued as inline
+// assembly, as dma16, so the compiler's wait insertion does not put a vmcnt
+// wait in front of later LDS reads; M0 is saved and restored.
+__device__ __forceinline__ void dma16_buf(i32x4 rsrc, uint32_t soff, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[lds]\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %[vo], %[rs], %[so] offen lds\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [rs] "s"(rsrc), [so] "s"(__builtin_amdgcn_readfirstlane(soff)), [vo] "v"(voff),
+        [lds] "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory");
+}
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+// Workgroup barrier that nothing is scheduled across (the phase boundaries of
+// the ping-pong K loop).
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Main loop: accumulates the (BN x BM) transposed tile into acc.
 // Wave (wm, wn) owns rows n in [wn*WN, +WN) and m in [wm*WM, +WM) of the tile.
 //
@@ -102,7 +148,9 @@ __device__ __forceinline__ void wait_lgkm0() {
 // WG > 0 (direct path only): the tile's W rows come in groups of WG rows,
 // group k starting at global row n0 + k * p.w_gstride (the q, k and v rows of
 // one head in the fused QKV weight); every row must exist.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT, int WG = 0>
+// PP (direct path, 256 x 256 tiles of 4 x 2 waves, BK 64, two stages, whole
+// tiles only): the ping-pong K loop, run_pingpong below.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIRECT, int WG = 0, bool PP = false>
 struct Mainloop {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = 64 * NW;
@@ -139,8 +187,150 @@ struct Mainloop {
 
   __device__ __forceinline__ static void run(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
     zero(acc);
-    if constexpr (DIRECT) run_direct(p, m0, n0, smem, acc);
+    if constexpr (PP) run_pingpong(p, m0, n0, smem, acc);
+    else if constexpr (DIRECT) run_direct(p, m0, n0, smem, acc);
     else run_staged(p, m0, n0, smem, acc);
+  }
+
+  // Ping-pong K loop.  Waves w and w + 4 share a SIMD; group 0 (waves 0-3,
+  // output columns 0-127 of the tile) and group 1 (waves 4-7, columns
+  // 128-255) run the same sequence one phase apart, a phase being the stretch
+  // between two workgroup barriers.  In its memory phase a wave reads the 24
+  // fragments of one K-tile from LDS into registers and issues its 8 copies
+  // (1 KB each, 4 of A rows and 4 of W rows); in its compute phase it issues
+  // that K-tile's 32 MFMAs and nothing else.  While one group computes, the
+  // other loads, so each SIMD has one wave feeding its matrix core.  A copy
+  // holds up its wave's issue for about 64-85 cycles (the vector-memory path
+  // moves ~64 B/clk per CU), so copies interleaved with a wave's MFMAs would
+  // stretch its compute phase; here they all sit in memory phases:
+  //   phase 2t    group 0: reads tile t (stage t&1), copies its share of
+  //                        tile t+1 into stage (t+1)&1, waits for its reads;
+  //               group 1: MFMAs of tile t-1;
+  //   phase 2t+1  group 0: MFMAs of tile t, then waits for its copies;
+  //               group 1: reads tile t, waits for them, copies its share of
+  //                        tile t+2 into stage t&1 (every read of that stage is
+  //                        done: group 0's before the last barrier, its own just
+  //                        now), waits until only those copies are in flight.
+  // Every copy of tile t+1 has landed when phase 2t+1 ends, before group 0
+  // reads it in phase 2t+2.  Tile 0 and group 1's share of tile 1 are copied
+  // before the loop.  Group 1 starts with one extra barrier and skips the one
+  // after its last compute phase, so both groups pass 2 * nk barriers.  Per
+  // accumulator the k order is run_direct's, so the results are bit-identical
+  // to it.
+  __device__ __forceinline__ static void run_pingpong(const GemmArgs& p, int m0, int n0, f16* smem,
+                                                      f32x16 (&acc)[FN][FM]) {
+    static_assert(BM == 256 && BN == 256 && WAVES_M == 4 && WAVES_N == 2 && BK == 64 && STAGES == 2 &&
+                      DIRECT && WG == 0 && A_INSTS == 4 && W_INSTS == 4,
+                  "ping-pong: 256 x 256 tile, 4 x 2 waves, BK 64, two stages");
+    constexpr int STAGE_BYTES = BM * BK * 2;  // one operand's K-tile: 32 KB
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % WAVES_M;
+    const int grp = wave / WAVES_M;  // = wn
+    const uint32_t lds_a = (uint32_t)(size_t)(lds_char*)smem + wave * A_INSTS * 1024;
+    const uint32_t lds_w = lds_a + STAGES * STAGE_BYTES;
+    const int nk = p.K / BK;  // even and at least 2 (the dispatch checks K > 0, K % 128 == 0)
+    // Copy c of a wave covers 8 rows (lane / 8 within them) of A (c < 4) or W;
+    // the lane fetches the logical chunk that the LDS swizzle stores at
+    // physical chunk lane % 8 of its row, (lane % 8) ^ ((row >> 1) & 7), which
+    // for these rows is (lane % 8) ^ (4 * (c & 1) + lane / 16).
+    uint32_t vo_a[2], vo_w[2];
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const uint32_t ch = (uint32_t)((lane & 7) ^ (4 * par + (lane >> 4)));
+      vo_a[par] = (uint32_t)((lane >> 3) * p.lda * 2) + (ch << 4);
+      vo_w[par] = (uint32_t)((lane >> 3) * p.ldw * 2) + (ch << 4);
+    }
+    // buffer bases: this wave's first copy row; byte offsets per copy and K-tile
+    const i32x4 rs_a = raw_buffer_rsrc(p.a + (int64_t)(m0 + wave * A_INSTS * 8) * p.lda);
+    const i32x4 rs_w = raw_buffer_rsrc(p.w + (int64_t)(n0 + wave * W_INSTS * 8) * p.ldw);
+    const uint32_t row8_a = (uint32_t)(16 * p.lda), row8_w = (uint32_t)(16 * p.ldw);  // 8 rows, bytes
+    auto copies = [&](int kt, int stage) {
+#pragma unroll
+      for (int c = 0; c < A_INSTS; ++c)
+        dma16_buf(rs_a, c * row8_a + kt * (BK * 2), vo_a[c & 1], lds_a + stage * STAGE_BYTES + c * 1024);
+#pragma unroll
+      for (int c = 0; c < W_INSTS; ++c)
+        dma16_buf(rs_w, c * row8_w + kt * (BK * 2), vo_w[c & 1], lds_w + stage * STAGE_BYTES + c * 1024);
+    };
+    // Fragment reads: lane byte offsets of k-step kk in the wave's first A and
+    // W row block of stage 0; the swizzle term depends on the row only
+    // through frow (block rows are multiples of 32), so the other blocks and
+    // stage 1 are constant byte offsets, folded into the ds_read immediates.
+    const int frow = lane & 31;
+    const int fhalf = lane >> 5;
+    uint32_t ra[KSTEPS], rw[KSTEPS];
+    {
+      const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        ra[kk] = lds0 + 2u * (uint32_t)swz<BK>(wm * WM + frow, 2 * kk + fhalf);
+        rw[kk] = lds0 + 2u * (uint32_t)(STAGES * BM * BK + swz<BK>(grp * WN + frow, 2 * kk + fhalf));
+      }
+    }
+    f16x8 fa[KSTEPS][FM], fw[KSTEPS][FN];
+    auto reads = [&](auto stage_c) {
+      constexpr int stage = decltype(stage_c)::value;
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          fa[kk][j] = *reinterpret_cast<const lds_f16x8*>(ra[kk] + (uint32_t)(2 * (stage * BM * BK + j * 32 * BK)));
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          fw[kk][i] = *reinterpret_cast<const lds_f16x8*>(rw[kk] + (uint32_t)(2 * (stage * BN * BK + i * 32 * BK)));
+      }
+    };
+    auto mfmas = [&]() {
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+        for (int x = 0; x < FM * FN; ++x) {
+          const int i = x / FM, j = x % FM;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[kk][i], fa[kk][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // K-tile t in stage t & 1 (compile-time: the loop runs two K-tiles per trip)
+    auto iter = [&](int t, auto stage_c) {
+      constexpr int stage = decltype(stage_c)::value;
+      // memory phase of tile t (group 0: phase 2t, group 1: phase 2t+1)
+      reads(stage_c);
+      __builtin_amdgcn_sched_barrier(0);
+      if (grp == 0) {
+        if (t + 1 < nk) copies(t + 1, stage ^ 1);
+        wait_lgkm0();  // this K-tile's reads are done before the barrier
+      } else {
+        wait_lgkm0();  // every read of this stage is done: it may be refilled
+        if (t + 2 < nk) {
+          copies(t + 2, stage);
+          wait_vmcnt<INSTS>();  // this wave's share of tile t+1 has landed
+        } else {
+          wait_vmcnt<0>();
+        }
+      }
+      phase_barrier();
+      // compute phase of tile t
+      mfmas();
+      __builtin_amdgcn_sched_barrier(0);
+      if (grp == 0) wait_vmcnt<0>();  // this wave's share of tile t+1 has landed
+      if (grp == 0 || t + 1 < nk) phase_barrier();
+    };
+
+    // tile 0 (every wave its share) and group 1's share of tile 1; then
+    // group 1 falls one phase behind
+    copies(0, 0);
+    if (grp == 1) {
+      copies(1, 1);
+      wait_vmcnt<INSTS>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    phase_barrier();
+    if (grp == 1) phase_barrier();
+    for (int t = 0; t < nk; t += 2) {
+      iter(t, IntC<0>{});
+      iter(t + 1, IntC<1>{});
+    }
   }
 
   __device__ __forceinline__ static void run_direct(const GemmArgs& p, int m0, int n0, f16* smem, f32x16 (&acc)[FN][FM]) {
@@ -359,13 +549,14 @@ struct Mainloop {
 // Tile configuration: block tile BM x BN, wave grid WAVES_M x WAVES_N, and
 // for the direct-copy path the K step and number of LDS stages.  The staged
 // (K-tail) path always runs K step 64 with two stages.
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_, int STAGES_, bool PP_ = false>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int BK = BK_, STAGES = STAGES_;
+  static constexpr bool PP = PP_;
   static constexpr int NT = 64 * WAVES_M_ * WAVES_N_;
   template <bool DIRECT>
-  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT>;
+  using ML = Mainloop<BM, BN, WAVES_M, WAVES_N, DIRECT ? BK : 64, DIRECT ? STAGES : 2, DIRECT, 0, PP && DIRECT>;
 };
 
 // Byte offset of 16-byte chunk `chunk` of row `row` in a row-major LDS
@@ -743,6 +934,7 @@ int launch_gemm(const GemmArgs& p, hipStream_t st) {
 }
 
 using TileBig = Tile<256, 256, 4, 2, 64, 2>;   // 8 waves of 64 x 128
+using TileBigPP = Tile<256, 256, 4, 2, 64, 2, true>;  // the same, ping-pong K loop (whole tiles)
 using TileMid = Tile<128, 128, 2, 2, 64, 2>;   // 4 waves of 64 x 64, 2 blocks per CU
 using TileSmall = Tile<64, 64, 1, 1, 64, 2>;   // 1 wave
 
@@ -762,7 +954,12 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   // 0.5-4 % faster in alternating same-box runs; larger K or more rounds
   // favour 256x256 (C3 FFN-down 141 vs 153 us, C3 QKV 116 vs 128 us).
   const bool short_k = p.K <= 1024 && t256 <= 512;
-  if (!short_k && t256 >= 256 && (t256 % 256 == 0 || t256 >= 512)) return launch_gemm<TileBig, EPI>(p, st);
+  if (!short_k && t256 >= 256 && (t256 % 256 == 0 || t256 >= 512)) {
+    // the ping-pong loop has no row clamp (whole tiles only) and runs K-tiles in pairs
+    // (measured: C4 forward 9.07 -> 8.62 ms, every 256 x 256 GEMM role 6-9 % faster)
+    if (p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0) return launch_gemm<TileBigPP, EPI>(p, st);
+    return launch_gemm<TileBig, EPI>(p, st);
+  }
   if (t128 >= 128) return launch_gemm<TileMid, EPI>(p, st);
   return launch_gemm<TileSmall, EPI>(p, st);
 }
