@@ -154,6 +154,7 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool DIR
 struct Mainloop {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = 64 * NW;
+  static constexpr bool PINGPONG = PP;
   static constexpr int WM = BM / WAVES_M;
   static constexpr int WN = BN / WAVES_N;
   static constexpr int FM = WM / 32;
@@ -581,7 +582,8 @@ constexpr int kEpiResidRows = 3;
 // own LDS region, row-major, then reads it back 16 bytes per lane along rows:
 // every global store then covers whole 128-byte lines instead of 16-byte
 // pieces of 32 rows.  Bias and GELU are applied in fp32 before the fp16
-// rounding.
+// rounding.  The caller has made the main-loop LDS free (every read of the
+// K-tile stages complete).
 template <class ML, int WAVES_M, int EPI>
 __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                int n0, f16* smem) {
@@ -596,7 +598,6 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
   const int mw = m0 + (wave % WAVES_M) * WM;
   const int nw = n0 + (wave / WAVES_M) * WN;
   char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
-  __syncthreads();  // every wave is done with the main-loop buffers
 #pragma unroll
   for (int jb = 0; jb < FM; jb += JC) {
 #pragma unroll
@@ -760,7 +761,8 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
 }
 
 // fp32 residual epilogue: one resid_pass per group of JC accumulator blocks
-// (two groups when the staging region holds one 32-row block per wave).
+// (two groups when the staging region holds one 32-row block per wave).  The
+// caller has made the main-loop LDS free.
 template <class ML, int WAVES_M, bool ROWS>
 __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                  int n0, f16* smem) {
@@ -773,7 +775,6 @@ __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16
   const int mw = m0 + (wave % WAVES_M) * ML::WM;
   const int nw = n0 + (wave / WAVES_M) * ML::WN;
   char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
-  __syncthreads();  // every wave is done with the main-loop buffers
   resid_pass<ML, WAVES_M, 0, JC, ROWS>(p, acc, mw, nw, region);
   if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC, ROWS>(p, acc, mw, nw, region);
 }
@@ -789,6 +790,12 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   f32x16 acc[ML::FN][ML::FM];
   ML::run(p, tm * BM, tn * BN, smem, acc);
+  // The epilogues stage each wave's results in its own part of the main-loop
+  // LDS.  The two-stage loop needs a barrier first (other waves may still read
+  // the last K-tile); after the ping-pong loop every read of the stages has
+  // completed before group 0's last barrier, so group 0 starts its epilogue
+  // while group 1 issues the last K-tile's MFMAs.
+  if constexpr (!ML::PINGPONG) __syncthreads();
   if constexpr (EPI == TK_EPI_BIAS_RESID || EPI == kEpiResidRows)
     store_tile_resid<ML, T::WAVES_M, EPI == kEpiResidRows>(p, acc, tm * BM, tn * BN, smem);
   else
