@@ -233,6 +233,54 @@ def gemm_yardstick(configs, reps: int) -> int:
     return 0
 
 
+def layernorm_rotated(configs, reps: int) -> int:
+    """Time the library's LayerNorm + cast (tk_ln_cast, fp32 -> fp16, and the
+    fp32-out final norm) at each config's [B*S, d_model] on SETS rotated buffer
+    sets, so no launch finds its input in the 256 MB Infinity Cache; the mean
+    of back-to-back launches between two events.  One JSON line per (config,
+    output dtype), with a plain device copy of the same bytes (read fp32,
+    write the output dtype) as the achievable reference."""
+    from tkmi import ops
+
+    dev = torch.device("cuda:0")
+    sets = 4
+    for name in configs:
+        b, s, d, _, _, _, _ = CONFIGS[name]
+        rows = b * s
+        w = torch.ones(d, device=dev)
+        bias = torch.zeros(d, device=dev)
+        xs = [torch.randn(rows, d, device=dev) for _ in range(sets)]
+        for out_dtype, per_el in ((torch.float16, 6), (torch.float32, 8)):
+            outs = [torch.empty(rows, d, dtype=out_dtype, device=dev) for _ in range(sets)]
+
+            def timed(fn):
+                # back-to-back launches between two events: no per-launch event overhead
+                for i in range(2 * sets):
+                    fn(i % sets)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for i in range(reps):
+                    fn(i % sets)
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) / reps
+
+            t_ln = timed(lambda i: ops.ln_fwd(xs[i], w, bias, 1e-5, out_dtype))  # noqa: B023
+            t_cp = timed(lambda i: outs[i].copy_(xs[i]))  # noqa: B023
+            nbytes = float(per_el * rows * d)
+            print(json.dumps({
+                "config": name, "rows": rows, "cols": d, "out_dtype": str(out_dtype).replace("torch.", ""),
+                "buffer_sets": sets, "bytes_per_launch": nbytes,
+                "ln_ms": round(t_ln, 5), "ln_frac_hbm": round(nbytes / (t_ln * 1e-3) / (PEAK_HBM_GBPS * 1e9), 4),
+                "copy_ms": round(t_cp, 5), "copy_frac_hbm": round(nbytes / (t_cp * 1e-3) / (PEAK_HBM_GBPS * 1e9), 4),
+            }), flush=True)
+            del outs
+        del xs
+        torch.cuda.empty_cache()
+    return 0
+
+
 def parse_shape(text: str) -> tuple:
     """``B,S,D,H,F,L[,causal|noncausal]`` -> (B, S, D, H, F, L, causal)."""
     parts = [t.strip() for t in text.split(",") if t.strip()]
@@ -336,6 +384,9 @@ def main() -> int:
     ap.add_argument("--gemm-yardstick", nargs="?", const="C3,C4,C5", default=None,
                     help="only time this build's GEMMs against hipBLASLt (F.linear) on the GEMM roles of the "
                          "given configs (default C3,C4,C5); one JSON line per role")
+    ap.add_argument("--layernorm-rotated", nargs="?", const="C2,C3,C4,C5", default=None,
+                    help="only time the LayerNorm + cast kernel on rotated buffers at the given configs' "
+                         "[B*S, d_model] (default C2,C3,C4,C5), beside a device copy of the same bytes")
     ap.add_argument("--unfused-norm", action="store_true",
                     help="residual GEMM + standalone LayerNorm instead of the fused GEMM+LN epilogue")
     args = ap.parse_args()
@@ -359,6 +410,12 @@ def main() -> int:
         if bad:
             raise SystemExit(f"--gemm-yardstick: unknown configs {bad}")
         return gemm_yardstick(names, max(args.steps, 3))
+    if args.layernorm_rotated:
+        names = [c.strip() for c in args.layernorm_rotated.split(",") if c.strip()]
+        bad = [c for c in names if c not in CONFIGS]
+        if bad:
+            raise SystemExit(f"--layernorm-rotated: unknown configs {bad}")
+        return layernorm_rotated(names, max(args.steps, 8))
 
     import tkmi
     from tkmi import ops

@@ -949,24 +949,24 @@ template <int EPI>
 int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  // Measured on MI355X (fp16, 256 CUs, every epilogue): 256x256 tiles win
-  // when they fill whole rounds of the 256 CUs (or at least two rounds);
-  // with a partial last round (e.g. 384 tiles) the 128x128 tile, two blocks
-  // per CU, is 5-10 % faster, as it is for narrow and short outputs down to
-  // 128 of its tiles; below that the 64x64 tile keeps the CUs busy.  (A
-  // 256x128 three-stage tile never won once the 128x128 tile was taken for
-  // narrow outputs, and is gone.)
-  // Short K (<= 1024) with at most two rounds of 256x256 tiles also runs
-  // 128x128 tiles (two blocks per CU): C2's FFN-up and C3's out-projection
-  // 0.5-4 % faster in alternating same-box runs; larger K or more rounds
-  // favour 256x256 (C3 FFN-down 141 vs 153 us, C3 QKV 116 vs 128 us).
+  // Measured on MI355X (fp16, 256 CUs, every epilogue).
+  // Whole 256x256 tiles (the ping-pong loop has no row clamp and runs K-tiles
+  // in pairs) that fill at least one round of the CUs take the ping-pong loop,
+  // short K included: C4 forward 9.07 -> 8.62 ms, every 256x256 GEMM role 6-9 %
+  // faster than the two-stage loop; C3 out-projection (one round, K = 1024)
+  // 62.0 -> 54.4 us against the 128x128 tile; C2 FFN-up (two rounds, K = 512)
+  // unchanged.
+  if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0)
+    return launch_gemm<TileBigPP, EPI>(p, st);
+  // Other shapes, with the two-stage loop: 256x256 tiles win when they fill
+  // whole rounds of the 256 CUs (or at least two rounds); with a partial last
+  // round (e.g. 384 tiles) the 128x128 tile, two blocks per CU, is 5-10 %
+  // faster, as it is for narrow and short outputs down to 128 of its tiles;
+  // below that the 64x64 tile keeps the CUs busy.  Short K (<= 1024) with at
+  // most two rounds of 256x256 tiles also runs 128x128 tiles (0.5-4 % faster);
+  // larger K or more rounds favour 256x256.
   const bool short_k = p.K <= 1024 && t256 <= 512;
-  if (!short_k && t256 >= 256 && (t256 % 256 == 0 || t256 >= 512)) {
-    // the ping-pong loop has no row clamp (whole tiles only) and runs K-tiles in pairs
-    // (measured: C4 forward 9.07 -> 8.62 ms, every 256 x 256 GEMM role 6-9 % faster)
-    if (p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0) return launch_gemm<TileBigPP, EPI>(p, st);
-    return launch_gemm<TileBig, EPI>(p, st);
-  }
+  if (!short_k && t256 >= 256 && (t256 % 256 == 0 || t256 >= 512)) return launch_gemm<TileBig, EPI>(p, st);
   if (t128 >= 128) return launch_gemm<TileMid, EPI>(p, st);
   return launch_gemm<TileSmall, EPI>(p, st);
 }
