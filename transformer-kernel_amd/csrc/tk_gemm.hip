@@ -583,8 +583,9 @@ constexpr int kEpiResidRows = 3;
 // every global store then covers whole 128-byte lines instead of 16-byte
 // pieces of 32 rows.  Bias and GELU are applied in fp32 before the fp16
 // rounding.  The caller has made the main-loop LDS free (every read of the
-// K-tile stages complete).
-template <class ML, int WAVES_M, int EPI>
+// K-tile stages complete).  WHOLE: the tile lies inside M x N, the output rows
+// take 16-byte stores and a given bias 16-byte loads (no bounds tests).
+template <class ML, int WAVES_M, int EPI, bool WHOLE>
 __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                int n0, f16* smem) {
   constexpr int WM = ML::WM, WN = ML::WN, FM = ML::FM, FN = ML::FN, NW = ML::NW;
@@ -608,7 +609,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
         const int n = nw + nl;
         if (p.bias) {
-          if (p.bias16 && n + 3 < p.N) {
+          if (WHOLE || (p.bias16 && n + 3 < p.N)) {
             const f32x4 b4 = *reinterpret_cast<const f32x4*>(p.bias + n);
             bv[0] = b4[0]; bv[1] = b4[1]; bv[2] = b4[2]; bv[3] = b4[3];
           } else {
@@ -643,10 +644,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
       const int row = idx / CPR, ch = idx % CPR;
       const int m = mw + jb * 32 + row;
       const int n = nw + ch * EPC;
-      if (m < p.M && n < p.N) {
+      if (WHOLE || (m < p.M && n < p.N)) {
         const f16x8 d = *reinterpret_cast<const f16x8*>(region + epi_off<CPR>(row, ch));
         f16* cr = reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n;
-        if (p.vec && n + 7 < p.N) {
+        if (WHOLE || (p.vec && n + 7 < p.N)) {
           *reinterpret_cast<f16x8*>(cr) = d;
         } else {
           for (int e = 0; e < 8 && n + e < p.N; ++e) cr[e] = d[e];
@@ -673,7 +674,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
 // given) the pass's JC * 32 validity bytes are loaded once, one per lane, and
 // their ballot is a wave-uniform bit mask; a lane tests its row's bit, and
 // an invalid row is written as resid (TK_ROWS_KEEP_RESID) or 0.
-template <class ML, int WAVES_M, int JB, int JC, bool ROWS>
+template <class ML, int WAVES_M, int JB, int JC, bool ROWS, bool WHOLE>
 __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int mw, int nw,
                                            char* region) {
   constexpr int FN = ML::FN;
@@ -686,7 +687,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
   const int lane = threadIdx.x & 63;
   const int ch = lane % CPR, row0 = lane / CPR;
   const int n = nw + ch * 4;
-  const bool vec = p.vec && n + 3 < p.N;
+  const bool vec = WHOLE || (p.vec && n + 3 < p.N);
   const int mb = mw + JB * 32;  // first row of the pass (wave-uniform)
   // wave-uniform base + 32-bit lane offsets (a pass spans 32 rows)
   const float* rbase = p.resid + (int64_t)mb * p.ldr + nw;
@@ -705,7 +706,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
     for (int it = 0; it < G; ++it) {
       const int row = (g * G + it) * RPI + row0;
       r[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (vec && mb + row < p.M) r[it] = *reinterpret_cast<const f32x4*>(rbase + ((uint32_t)row * ldr + ch * 4));
+      if (vec && (WHOLE || mb + row < p.M)) r[it] = *reinterpret_cast<const f32x4*>(rbase + ((uint32_t)row * ldr + ch * 4));
     }
   };
   auto combine = [&](int g, const f32x4& b) {
@@ -713,7 +714,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
     for (int it = 0; it < G; ++it) {
       const int row = (g * G + it) * RPI + row0;
       const int m = mb + row;
-      if (m < p.M && n < p.N) {
+      if (WHOLE || (m < p.M && n < p.N)) {
         const f32x4 d = *reinterpret_cast<const f32x4*>(region + epi_off<CPR>(row, ch));
         float* cr = reinterpret_cast<float*>(p.c) + (int64_t)m * p.ldc + n;
         const bool valid = !ROWS || ((rows_ok >> row) & 1ull);
@@ -733,7 +734,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
 
   f32x4 b = {0.f, 0.f, 0.f, 0.f};
   if (p.bias && vec) {
-    if (p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
+    if (WHOLE || p.bias16) b = *reinterpret_cast<const f32x4*>(p.bias + n);
     else b = f32x4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
   }
   if constexpr (EARLY) fetch(0);
@@ -763,7 +764,7 @@ __device__ __forceinline__ void resid_pass(const GemmArgs& p, const f32x16 (&acc
 // fp32 residual epilogue: one resid_pass per group of JC accumulator blocks
 // (two groups when the staging region holds one 32-row block per wave).  The
 // caller has made the main-loop LDS free.
-template <class ML, int WAVES_M, bool ROWS>
+template <class ML, int WAVES_M, bool ROWS, bool WHOLE>
 __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                  int n0, f16* smem) {
   constexpr int FM = ML::FM, NW = ML::NW;
@@ -775,8 +776,8 @@ __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16
   const int mw = m0 + (wave % WAVES_M) * ML::WM;
   const int nw = n0 + (wave / WAVES_M) * ML::WN;
   char* region = reinterpret_cast<char*>(smem) + wave * (JC * 32 * ROWB);
-  resid_pass<ML, WAVES_M, 0, JC, ROWS>(p, acc, mw, nw, region);
-  if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC, ROWS>(p, acc, mw, nw, region);
+  resid_pass<ML, WAVES_M, 0, JC, ROWS, WHOLE>(p, acc, mw, nw, region);
+  if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC, ROWS, WHOLE>(p, acc, mw, nw, region);
 }
 
 template <class T, int EPI, bool DIRECT>
@@ -797,9 +798,9 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   // while group 1 issues the last K-tile's MFMAs.
   if constexpr (!ML::PINGPONG) __syncthreads();
   if constexpr (EPI == TK_EPI_BIAS_RESID || EPI == kEpiResidRows)
-    store_tile_resid<ML, T::WAVES_M, EPI == kEpiResidRows>(p, acc, tm * BM, tn * BN, smem);
+    store_tile_resid<ML, T::WAVES_M, EPI == kEpiResidRows, ML::PINGPONG>(p, acc, tm * BM, tn * BN, smem);
   else
-    store_tile_lds<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem);
+    store_tile_lds<ML, T::WAVES_M, EPI, ML::PINGPONG>(p, acc, tm * BM, tn * BN, smem);
 }
 
 // Full-row variant: BN == N, so each block owns complete output rows and
@@ -956,7 +957,9 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   // faster than the two-stage loop; C3 out-projection (one round, K = 1024)
   // 62.0 -> 54.4 us against the 128x128 tile; C2 FFN-up (two rounds, K = 512)
   // unchanged.
-  if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0)
+  // (its epilogues also assume vector-aligned output rows and bias).
+  if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0 && p.vec &&
+      (p.bias == nullptr || p.bias16))
     return launch_gemm<TileBigPP, EPI>(p, st);
   // Other shapes, with the two-stage loop: 256x256 tiles win when they fill
   // whole rounds of the 256 CUs (or at least two rounds); with a partial last
