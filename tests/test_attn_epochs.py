@@ -139,7 +139,7 @@ class Ins:
             self.reads = {"m0"}
         elif op.startswith("s_") and ops and ops[0] == "m0":
             self.writes = {"m0"}
-        elif op == "s_cbranch_vccz":
+        elif op in ("s_cbranch_vccz", "s_cbranch_vccnz"):
             self.reads = {"vcc"}
         self.target = ops[0] if op.startswith("s_cbranch") or op == "s_branch" else None
 
@@ -176,7 +176,7 @@ def _rule(prod: Ins, cons: Ins, reg: str) -> int:
     if reg == "m0":
         return 1 if c.startswith("global_load_lds") else 0
     if reg == "vcc":
-        return 4 if c == "s_cbranch_vccz" else 0
+        return 4 if c in ("s_cbranch_vccz", "s_cbranch_vccnz") else 0
     if c.startswith("v_permlane32_swap") and p.startswith("v_"):
         return 2 if reg in cons.reads else 0
     return 0
@@ -231,9 +231,10 @@ def test_wait_state_checker_finds_planted_mistakes(planted):
         src = prog[i].split(", ")[-1]
         j = max(k for k in range(i) if prog[k] == f"v_exp_f32 {src}, {src}")
         prog.insert(j + 1, prog[i])
-    elif planted == "mfma":  # row max right after the score MFMAs
-        i = next(i for i, l in enumerate(prog) if l.startswith("v_max3_f32"))
-        del prog[i - 3:i]
+    elif planted == "mfma":  # a score read right after the MFMA that writes it
+        sb = f"v[{gen.SB1}:{gen.SB1 + 15}]"
+        i = next(i for i, l in enumerate(prog) if l.startswith(f"v_mfma_f32_32x32x16_f16 {sb}"))
+        prog.insert(i + 1, f"v_max_f32 v{gen.T0}, v{gen.T0}, v{gen.SB1}")
     elif planted == "m0":
         i = next(i for i, l in enumerate(prog) if l.startswith("global_load_lds"))
         assert prog[i - 1] == "s_nop 0"
@@ -261,10 +262,57 @@ def test_loop_registers_stay_in_its_operands_and_clobbers(loop):
 
 
 def test_loop_covers_four_epochs_of_32_mfmas():
-    prog = gen.program()
-    assert sum(1 for l in prog if l.startswith("v_mfma")) == 4 * 32
-    assert sum(1 for l in prog if l == "s_barrier") == 4
-    assert sum(1 for l in prog if l.startswith("global_load_lds")) == 4 * 4
+    for prog, extra in ((gen.one_phase_program(), 0), (gen.program(), 1)):  # + S(1) before the loop
+        assert sum(1 for l in prog if l.startswith("v_mfma")) == 4 * 32 + 16 * extra
+        assert sum(1 for l in prog if l == "s_barrier") == 4 + extra
+        assert sum(1 for l in prog if l.startswith("global_load_lds")) == 4 * 4
+
+
+def _slots(iteration: list[str]) -> list[list[str]]:
+    """An iteration cut at its MFMAs: slot s = the MFMA of slot s and what follows it."""
+    out = [[]]
+    for l in iteration:
+        if l.startswith("v_mfma"):
+            out.append([])
+        out[-1].append(l)
+    return out[1:]
+
+
+@pytest.mark.parametrize("u", range(4))
+def test_spread_loop_reads_each_score_before_it_is_replaced(u):
+    """The dense loop's iteration u: key-block-1 scores of S(e) (SB1) are all read before the
+    first MFMA of S(e+1) key block 1 overwrites them (slot 24); P(e-1) (region Y) is read by
+    the 16 P.V MFMAs before S(e+1) key block 0 overwrites it (slot 16); every score register
+    is scaled, exponentiated and packed in that order, pairs in order, each P register packed
+    after the score in it was consumed; the row sums add P registers 0..15 in order."""
+    X, Y = (gen.P[1], gen.P[0]) if u % 2 == 0 else (gen.P[0], gen.P[1])
+    sl = _slots(gen.spread_iteration(u))
+    assert len(sl) == 32
+    sb = {f"v{r}" for r in range(gen.SB1, gen.SB1 + 16)}
+    y = {f"v{r}" for r in range(Y, Y + 16)}
+    for s, slot in enumerate(sl):
+        for x in map(Ins, slot):
+            if x.op.startswith("v_mfma"):
+                assert (y <= x.writes) == (16 <= s < 24) and (sb <= x.writes) == (s >= 24), (s, x.text)
+                if s < 16:
+                    assert x.reads & y
+            elif x.reads & sb:
+                assert s < 24, (s, x.text)
+    body = [Ins(l) for l in gen.spread_iteration(u) if not l.startswith(("v_mfma", "s_", "ds_", "global_"))]
+    score = lambda i: f"v{X + i}" if i < 16 else f"v{gen.SB1 + i - 16}"
+    seq = {score(i): [] for i in range(32)}
+    packs = []
+    for x in body:
+        if x.op in ("v_fma_f32", "v_exp_f32"):
+            (r,) = x.writes
+            seq[r].append(x.op)
+        elif x.op == "v_cvt_pk_f16_f32":
+            packs.append(x)
+    assert all(ops == ["v_fma_f32", "v_exp_f32"] for ops in seq.values())
+    assert [sorted(p.reads) for p in packs] == [sorted({score(2 * j), score(2 * j + 1)}) for j in range(16)]
+    assert [next(iter(p.writes)) for p in packs] == [f"v{X + j}" for j in range(16)]
+    dots = [x for x in body if x.op == "v_dot2c_f32_f16"]
+    assert [sorted(x.reads - {f"v{gen.LS}"}) for x in dots] == [[f"v{X + j}"] for j in range(16)]
 
 
 def test_hd64_loop_covers_two_steps_of_16_mfmas():
@@ -289,9 +337,9 @@ def test_hd64_loops_differ_only_in_the_copies():
 
 
 def test_key_masked_loop_adds_only_the_mask_work():
-    """The key-masked loop is the dense one plus, per epoch, the validity-byte load,
+    """The key-masked loop is the one-phase dense loop plus, per epoch, the validity-byte load,
     the key bits, 32 score selects and the m = -inf guard."""
-    dense, masked = gen.program(False), gen.program(True)
+    dense, masked = gen.one_phase_program(False), gen.program(True)
     extra = [l for l in masked if l not in dense]
     assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "s_waitcnt vmcnt(4)", "v_cmp_",
                              "s_mov_b32 s9", "s_mov_b64 s[94:95]", "s_bfe_i32", "v_cndmask_b32",

@@ -1,11 +1,13 @@
-"""Emit tk_attn_epochs.inc: the hand-ordered steady-state epochs of the head_dim-128 causal
-attention (flash_pair_body in tk_attention.hip, 8 waves, 256 query rows per workgroup).
+"""Emit tk_attn_epochs.inc and tk_attn_epochs_kmask.inc: the hand-ordered steady-state epochs of
+the head_dim-128 causal attention (flash_pair_body in tk_attention.hip, 8 waves, 256 query rows
+per workgroup), without and with a key mask.
 
-    python gen_attn_epochs.py [out.inc]      # default: tk_attn_epochs.inc beside this file
+    python gen_attn_epochs.py [outdir]      # default: beside this file
 
-The build runs this before compiling tk_attention.hip, so the .inc and this script cannot drift.
+The build runs this before compiling tk_attention.hip, so the .inc files and this script cannot
+drift.
 
-What the loop computes
+What an epoch computes
 ----------------------
 Epoch e of the pair body (key tile e = keys 64e .. 64e+63) does, for every wave:
 
@@ -31,10 +33,26 @@ row whose m_new would be -inf.  The rescale still maps m_new = -inf to alpha = 1
 one select on that rare path), so l and O cannot turn into NaN if the loop's gate ever admits
 rows with different key histories.
 
+The key-masked loop (one_phase_program) runs each epoch in that order.  The dense loop
+(program_spread) computes the same operations per lane in the same order, but software-pipelined
+so that every one of an iteration's 32 MFMA slots carries a share of the softmax: iteration e
+runs the P.V MFMAs of epoch e (slots 0..15) and the score MFMAs of epoch e+1 (key block 0 in
+slots 16..23, key block 1 in 24..31); between them the row max and rescale test of S(e)
+(slots 0..2), the 16 exponential pairs of S(e), computed in place on the score registers
+(slots 3..23), and the row sums in pair order plus the key-block-0 max of S(e+1) (24..31).  The
+scores of epoch 1 are computed before the loop; the last iteration also computes the scores of
+the epoch after the loop, which the compiled epoch recomputes (16 MFMAs per loop).  Two waves of
+a SIMD issuing MFMAs with at most about three VALU instructions and one exponential between
+each pair run at the MFMA rate; the one-phase epoch, with its 32 exponentials between 16 of its
+MFMAs and none between the other 16, cannot hide them.
+
 One loop iteration is 4 epochs, so epoch e = 1 + 4i + u (loop position u) reads V(e-1) from
 V slot (e-1) % 4 = u and writes V(e+1) into slot (u + 2) % 4: both are immediate LDS offsets.
 The K ring has 3 slots, so its read and write slots rotate through the SGPR trackers krd and kwr
-(byte offsets of the slots, starting at slots 1 and 0 for epoch 1).
+(byte offsets of the slots, starting at slots 1 and 0 for epoch 1).  The dense loop reads K(e+1)
+in iteration e, so it waits at the end of iteration e for the K copy of that iteration
+(vmcnt(2): the V copies, issued after it, may stay in flight) and advances krd once after the
+scores of epoch 1.
 
 Register map (all VGPRs; the asm statement pins or clobbers every one of them)
 -------------------------------------------------------------------------------
@@ -47,10 +65,15 @@ Register map (all VGPRs; the asm statement pins or clobbers every one of them)
               max phases use MX/TMP, the P.V phase T0/T1)
   v[198:213]  scores, key block 1                 (clobbered)
   v[214:225]  operand ring, 3 x 4: K fragments in the S phase, V fragments in the P.V phase
-  v[226:227]  second temporary pair of the exponential pipeline (clobbered)
+  v[226:227]  second temporary pair of the exponential pipeline (clobbered); in the dense loop
+              the K read address and its base (krd + kl0)
 Scores of key block 0 live in the region that receives the new P tile: P.V step c writes P
 register c after reading scores 2c and 2c+1, and score c was read at step c // 2.  Regions A and
-B alternate between "P being consumed" and "scores block 0 / new P" from epoch to epoch.
+B alternate between "P being consumed" and "scores block 0 / new P" from epoch to epoch.  The
+dense loop exponentiates in place (score register -> scaled -> exp2 -> packed into P register j),
+so it needs no temporary pairs; its score MFMAs of epoch e+1 write key block 0 into the region P
+of epoch e-1 leaves (after the P.V MFMAs that read it) and key block 1 into v[198:213] (after
+the last exponential pair of epoch e has read it).
 
 Wait states given for the hazards the hardware does not interlock (each at least what the
 compiler inserts for gfx950 in the same situation)
@@ -248,8 +271,218 @@ def epoch(u: int, kmask: bool = False) -> list[str]:
     return L
 
 
+# --------------------------------------------------------------------------- #
+# the dense loop: softmax work spread over all 32 MFMA slots of an iteration
+# --------------------------------------------------------------------------- #
+# Relative VALU issue cost of one instruction (cycles of a lone wave): exponentials occupy the
+# transcendental unit about 8.6 cycles, the rest about 5.3.  Used only to spread the work evenly.
+def _cost(ins: str) -> float:
+    return 8.6 if ins.startswith("v_exp") else 5.3 if ins.startswith("v_") else 1.0
+
+
+def _spread(ops: list[str], slots: list[list[str]], first: int, last: int) -> None:
+    """Append the instructions, in order, to slots first..last, cutting the stream by issue cost."""
+    total = sum(_cost(i) for i in ops)
+    n, acc = last - first + 1, 0.0
+    for i in ops:
+        slots[min(first + int((acc + _cost(i) / 2) * n / total), last)].append(i)
+        acc += _cost(i)
+
+
+def block0_max(x: int) -> list[str]:
+    """MX = max of the key-block-0 scores (accumulator entries x .. x+15)."""
+    L = [f"v_max3_f32 {v(MX)}, {v(x)}, {v(x + 1)}, {v(x + 2)}"]
+    L += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(x + k)}, {v(x + k + 1)}" for k in range(3, 15, 2)]
+    return L + [f"v_max_f32 {v(MX)}, {v(MX)}, {v(x + 15)}"]
+
+
+def spread_iteration(u: int) -> list[str]:
+    """Iteration at loop position u (epoch e = 1 + 4i + u) of the dense loop.
+
+    MFMA slots 0..15: O^T += V^T(e-1) P^T(e-1) (head-dim block c & 3, P block c >> 2);
+    slots 16..23: S^T(e+1) key block 0 (k-steps 0..7), slots 24..31: key block 1 (k-steps 0..7).
+    VALU work between them: the key-block-1 half of the row max of S(e), the lane-pair max and
+    the rescale test (slots 0..2; the key-block-0 half ran in slots 26..31 of the iteration
+    before); the 16 exponential pairs of S(e), each computed in place on its two score
+    registers and packed into P register j (slots 3..23: the pairs of key block 1 read SB1,
+    which the key-block-1 MFMAs of S(e+1) overwrite from slot 24, and pair j's pack overwrites
+    the score register of pair j // 2, so the pairs run in order); the fp16 row sums in pair
+    order and the key-block-0 max of S(e+1) (slots 24..31).
+    """
+    X, Y = (P[1], P[0]) if u % 2 == 0 else (P[0], P[1])  # X: S(e) key block 0 -> P(e); Y: P(e-1)
+    KB, KA = TX + 1, TX  # K read base (krd + kl0) and the XOR-swizzled address of one k-step
+
+    def sr(i: int) -> int:
+        return X + i if i < 16 else SB1 + (i - 16)
+
+    def ring(s: int) -> int:
+        return RING + 4 * (s % 3)
+
+    vslot = u * TILE
+
+    def read(s: int) -> list[str]:
+        """Operand of MFMA slot s into ring entry s % 3."""
+        if s < 16:
+            t, d = s >> 2, s & 3
+            return [f"ds_read_b64_tr_b16 {v(ring(s), 2)}, %[vl{d}] offset:{vslot + t * 4096}",
+                    f"ds_read_b64_tr_b16 {v(ring(s) + 2, 2)}, %[vl{d}] offset:{vslot + t * 4096 + 2048}"]
+        f = s - 16
+        blk, kk = f >> 3, f & 7
+        # k-step kk reads chunk 2kk + g of the XOR-swizzled row: (krd + kl0) ^ (kk << 5), as krd
+        # is a multiple of the 16 KiB tile and the swizzle touches bits 5..7 only
+        if kk == 0:
+            return [f"ds_read_b128 {v(ring(s), 4)}, {v(KB)} offset:{blk * 8192}"]
+        return [f"v_xor_b32 {v(KA)}, {kk << 5}, {v(KB)}",
+                f"ds_read_b128 {v(ring(s), 4)}, {v(KA)} offset:{blk * 8192}"]
+
+    def n_ds(s: int) -> int:
+        return 2 if s < 16 else 1
+
+    def mfma(s: int) -> str:
+        if s < 16:
+            c = s
+            return (f"v_mfma_f32_32x32x16_f16 {v(O + 16 * (c & 3), 16)}, {v(ring(s), 4)}, "
+                    f"{v(Y + 4 * (c >> 2), 4)}, {v(O + 16 * (c & 3), 16)}")
+        f = s - 16
+        dst = Y if f < 8 else SB1
+        kk = f & 7
+        src_c = "0" if kk == 0 else v(dst, 16)
+        return f"v_mfma_f32_32x32x16_f16 {v(dst, 16)}, {v(ring(s), 4)}, {v(Q + 4 * kk, 4)}, {src_c}"
+
+    slots: list[list[str]] = [[] for _ in range(32)]
+    # ---- row max of S(e): MX holds key block 0's; key block 1's, the lane pair, rescale test ----
+    mx = [f"v_max3_f32 {v(TMP)}, {v(sr(16))}, {v(sr(17))}, {v(sr(18))}"]
+    mx += [f"v_max3_f32 {v(TMP)}, {v(TMP)}, {v(sr(16 + k))}, {v(sr(17 + k))}" for k in range(3, 15, 2)]
+    mx += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(31))}, {v(TMP)}",
+           f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1", f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
+           f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
+           f"v_mul_f32 {v(MX)}, %[cs], {v(MX)}",                 # m_tile
+           f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",            # m_run + 8
+           f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
+           f"s_cbranch_vccnz L_rescale_{u}_%=", f"L_rescaled_{u}_%=:"]
+    for k in range(3):
+        slots[k] += mx[len(mx) * k // 3:len(mx) * (k + 1) // 3]
+
+    # ---- exponential pairs, in place: s -> s * cs - m_run -> exp2 -> fp16 pair in P register j ----
+    def scale(j: int) -> list[str]:
+        return [f"v_fma_f32 {v(sr(i))}, {v(sr(i))}, %[cs], -{v(MR)}" for i in (2 * j, 2 * j + 1)]
+
+    def expo(j: int) -> list[str]:
+        return [f"v_exp_f32 {v(sr(i))}, {v(sr(i))}" for i in (2 * j, 2 * j + 1)]
+
+    def pack(j: int) -> list[str]:
+        # P register j = score register j, whose pair (j // 2) is done: pairs run in order
+        return [f"v_cvt_pk_f16_f32 {v(X + j)}, {v(sr(2 * j))}, {v(sr(2 * j + 1))}"]
+
+    stream = []
+    for t in range(18):  # pair t scaled, pair t-1 exponentiated, pair t-2 packed
+        if t < 16:
+            stream += scale(t)
+        if 0 <= t - 1 < 16:
+            stream += expo(t - 1)
+        if 0 <= t - 2 < 16:
+            stream += pack(t - 2)
+    _spread(stream, slots, 3, 23)
+    # ---- fp16 row sums (dot2 with 1.0h) in pair order 0..15; key block 0's max of S(e+1) ----
+    _spread([f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(X + j)}" for j in range(16)], slots, 24, 31)
+    _spread(block0_max(Y), slots, 26, 31)
+    # ---- copies: K(e+2) into the K slot kwr (before the iteration's vmcnt), V(e+1) into V slot
+    # (u + 2) % 4; the K read base for S(e+1) ----
+    vw = (3 + (u + 2) % 4) * TILE
+    slots[0] = ["s_add_u32 m0, %[ldsw], %[kwr]", "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
+                "v_add_u32 %[ko0], %[kt2], %[ko0]"] + slots[0]
+    slots[2] = ["s_add_u32 m0, %[ldsw], %[kwr]", "s_add_u32 m0, m0, 8192", "s_nop 0",
+                "global_load_lds_dwordx4 %[ko1], %[kb]", "v_add_u32 %[ko1], %[kt2], %[ko1]"] + slots[2]
+    slots[25] += [f"s_add_u32 m0, %[ldsw], {vw}", "s_nop 0", "global_load_lds_dwordx4 %[vo0], %[vb]",
+                  "v_add_u32 %[vo0], %[vt2], %[vo0]"]
+    slots[28] += [f"s_add_u32 m0, %[ldsw], {vw + 8192}", "s_nop 0", "global_load_lds_dwordx4 %[vo1], %[vb]",
+                  "v_add_u32 %[vo1], %[vt2], %[vo1]"]
+    slots[11] += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]
+
+    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"] + read(0) + read(1)
+    for s in range(32):
+        if s + 2 < 32:
+            L += read(s + 2)
+        pending = sum(n_ds(k) for k in range(s + 1, min(32, s + 3)))
+        L.append(f"s_waitcnt lgkmcnt({pending})")
+        L.append(mfma(s))
+        L += slots[s]
+    L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
+    L += ["s_cmp_lg_u32 %[flag], 0", f"s_cbranch_scc1 L_oscale_{u}_%=", f"L_oscaled_{u}_%=:"]
+    # ---- end: K(e+2) has landed (the V copies may stay in flight), barrier ----
+    L += ["s_waitcnt vmcnt(2)", "s_barrier",
+          "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
+          "s_add_u32 %[kwr], %[kwr], 16384", "s_cmp_eq_u32 %[kwr], 49152", "s_cselect_b32 %[kwr], 0, %[kwr]"]
+    return L
+
+
+def spread_out_of_line(u: int) -> list[str]:
+    """The rare paths of iteration u, placed after the loop: the lazy rescale and O *= alpha."""
+    L = [f"L_rescale_{u}_%=:",
+         f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",               # m_new
+         f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
+         f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
+         f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",              # m_new = -inf: alpha = 1
+         f"v_mov_b32 {v(MR)}, {v(TMP)}",
+         f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
+         f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
+         "s_mov_b32 %[flag], 1", f"s_branch L_rescaled_{u}_%="]
+    L += [f"L_oscale_{u}_%=:"]
+    L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(64)]
+    L += [f"s_branch L_oscaled_{u}_%="]
+    return L
+
+
+def program_spread() -> list[str]:
+    """The dense asm body: S(1) first, then `groups` iterations of 4 epochs, each computing the
+    scores of the epoch after it; the rare paths after the loop."""
+    L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]",
+         "s_mov_b32 %[krd], %[krd0]", "s_mov_b32 %[kwr], %[kwr0]", "s_nop 1"]
+    # ---- S(1) = K(1) . Q^T: key block 0 into P region B, key block 1 into SB1 ----
+    KB, KA = TX + 1, TX
+    L += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]
+
+    def kread(f: int) -> list[str]:
+        blk, kk = f >> 3, f & 7
+        if kk == 0:
+            return [f"ds_read_b128 {v(RING + 4 * (f % 3), 4)}, {v(KB)} offset:{blk * 8192}"]
+        return [f"v_xor_b32 {v(KA)}, {kk << 5}, {v(KB)}",
+                f"ds_read_b128 {v(RING + 4 * (f % 3), 4)}, {v(KA)} offset:{blk * 8192}"]
+
+    L += kread(0) + kread(1)
+    for f in range(16):
+        if f + 2 < 16:
+            L += kread(f + 2)
+        L.append(f"s_waitcnt lgkmcnt({min(2, 15 - f)})")
+        dst = P[1] if f < 8 else SB1
+        src_c = "0" if f & 7 == 0 else v(dst, 16)
+        L.append(f"v_mfma_f32_32x32x16_f16 {v(dst, 16)}, {v(RING + 4 * (f % 3), 4)}, "
+                 f"{v(Q + 4 * (f & 7), 4)}, {src_c}")
+    # K(2) and V(1), copied by the epoch before the loop, land for every wave; K(2) is next
+    L += ["s_waitcnt vmcnt(0)", "s_barrier",
+          "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
+          "s_nop 7", "s_nop 7", "s_nop 7"]
+    L += block0_max(P[1])
+    L += ["L_epochs_%=:"]
+    for u in range(4):
+        L += spread_iteration(u)
+    L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_epochs_%=",
+          "s_branch L_done_%="]
+    for u in range(4):
+        L += spread_out_of_line(u)
+    # the compiled code after the statement reads O and reuses the score registers: MFMA
+    # result latency first
+    L += ["L_done_%=:", "s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    return L
+
+
 def program(kmask: bool = False) -> list[str]:
-    """The whole asm body: M0 saved, `groups` iterations of 4 epochs, M0 restored."""
+    """The asm body of the loop the kernel runs: the spread dense loop, or the key-masked one."""
+    return one_phase_program(True) if kmask else program_spread()
+
+
+def one_phase_program(kmask: bool = False) -> list[str]:
+    """The one-phase asm body: M0 saved, `groups` iterations of 4 epochs, M0 restored."""
     L = ["s_mov_b32 %[msave], m0", "s_mov_b32 %[cnt], %[groups]",
          "s_mov_b32 %[krd], %[krd0]", "s_mov_b32 %[kwr], %[kwr0]", "s_nop 1"]
     L += ["L_epochs_%=:"]
