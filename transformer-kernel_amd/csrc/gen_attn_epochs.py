@@ -52,7 +52,9 @@ The K ring has 3 slots, so its read and write slots rotate through the SGPR trac
 (byte offsets of the slots, starting at slots 1 and 0 for epoch 1).  The dense loop reads K(e+1)
 in iteration e, so it waits at the end of iteration e for the K copy of that iteration
 (vmcnt(2): the V copies, issued after it, may stay in flight) and advances krd once after the
-scores of epoch 1.
+scores of epoch 1.  It copies V two epochs ahead (V(e+2) into V slot (e+2) % 4, which held
+V(e-2); V(2) before the loop), so V(e) has landed and passed a barrier by the end of iteration
+e, whose last two slots already read the first two V(e) fragments of the next iteration.
 
 Register map (all VGPRs; the asm statement pins or clobbers every one of them)
 -------------------------------------------------------------------------------
@@ -296,6 +298,14 @@ def block0_max(x: int) -> list[str]:
     return L + [f"v_max_f32 {v(MX)}, {v(MX)}, {v(x + 15)}"]
 
 
+def vread(c: int, u: int) -> list[str]:
+    """V fragment c of the P.V MFMAs at loop position u (V slot u) into ring entry c % 3; the
+    second half-fragment sits 8 tile rows (2048 bytes) further, same swizzle."""
+    t, d, base = c >> 2, c & 3, RING + 4 * (c % 3)
+    return [f"ds_read_b64_tr_b16 {v(base, 2)}, %[vl{d}] offset:{u * TILE + t * 4096}",
+            f"ds_read_b64_tr_b16 {v(base + 2, 2)}, %[vl{d}] offset:{u * TILE + t * 4096 + 2048}"]
+
+
 def spread_iteration(u: int) -> list[str]:
     """Iteration at loop position u (epoch e = 1 + 4i + u) of the dense loop.
 
@@ -318,15 +328,13 @@ def spread_iteration(u: int) -> list[str]:
     def ring(s: int) -> int:
         return RING + 4 * (s % 3)
 
-    vslot = u * TILE
-
     def read(s: int) -> list[str]:
-        """Operand of MFMA slot s into ring entry s % 3."""
-        if s < 16:
-            t, d = s >> 2, s & 3
-            return [f"ds_read_b64_tr_b16 {v(ring(s), 2)}, %[vl{d}] offset:{vslot + t * 4096}",
-                    f"ds_read_b64_tr_b16 {v(ring(s) + 2, 2)}, %[vl{d}] offset:{vslot + t * 4096 + 2048}"]
-        f = s - 16
+        """Operand of MFMA slot s into ring entry s % 3; slots 32 and 33 are the next iteration's
+        0 and 1 (V(e) from V slot (u + 1) % 4, issued after MFMAs 30 and 31 free their entries)."""
+        return vread(s, u) if s < 16 else vread(s - 32, (u + 1) % 4) if s >= 32 else kread(s - 16)
+
+    def kread(f: int) -> list[str]:
+        s = 16 + f
         blk, kk = f >> 3, f & 7
         # k-step kk reads chunk 2kk + g of the XOR-swizzled row: (krd + kl0) ^ (kk << 5), as krd
         # is a multiple of the 16 KiB tile and the swizzle touches bits 5..7 only
@@ -334,9 +342,6 @@ def spread_iteration(u: int) -> list[str]:
             return [f"ds_read_b128 {v(ring(s), 4)}, {v(KB)} offset:{blk * 8192}"]
         return [f"v_xor_b32 {v(KA)}, {kk << 5}, {v(KB)}",
                 f"ds_read_b128 {v(ring(s), 4)}, {v(KA)} offset:{blk * 8192}"]
-
-    def n_ds(s: int) -> int:
-        return 2 if s < 16 else 1
 
     def mfma(s: int) -> str:
         if s < 16:
@@ -386,9 +391,9 @@ def spread_iteration(u: int) -> list[str]:
     # ---- fp16 row sums (dot2 with 1.0h) in pair order 0..15; key block 0's max of S(e+1) ----
     _spread([f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(X + j)}" for j in range(16)], slots, 24, 31)
     _spread(block0_max(Y), slots, 26, 31)
-    # ---- copies: K(e+2) into the K slot kwr (before the iteration's vmcnt), V(e+1) into V slot
-    # (u + 2) % 4; the K read base for S(e+1) ----
-    vw = (3 + (u + 2) % 4) * TILE
+    # ---- copies: K(e+2) into the K slot kwr (before the iteration's vmcnt), V(e+2) into V slot
+    # (u + 3) % 4 (it held V(e-2), last read in the iteration before); the K read base ----
+    vw = (3 + (u + 3) % 4) * TILE
     slots[0] = ["s_add_u32 m0, %[ldsw], %[kwr]", "s_nop 0", "global_load_lds_dwordx4 %[ko0], %[kb]",
                 "v_add_u32 %[ko0], %[kt2], %[ko0]"] + slots[0]
     slots[2] = ["s_add_u32 m0, %[ldsw], %[kwr]", "s_add_u32 m0, m0, 8192", "s_nop 0",
@@ -399,13 +404,20 @@ def spread_iteration(u: int) -> list[str]:
                   "v_add_u32 %[vo1], %[vt2], %[vo1]"]
     slots[11] += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]
 
-    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"] + read(0) + read(1)
+    # the reads of slots 0 and 1 were issued by the iteration before (or the scores of epoch 1)
+    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    issued = [0, 0, 1, 1]  # slot of every LDS read in flight, in issue order
     for s in range(32):
         if s + 2 < 32:
             L += read(s + 2)
-        pending = sum(n_ds(k) for k in range(s + 1, min(32, s + 3)))
-        L.append(f"s_waitcnt lgkmcnt({pending})")
+            issued += [s + 2] * sum(1 for l in read(s + 2) if l.startswith("ds_"))
+        last = max(i for i, k in enumerate(issued) if k == s)
+        L.append(f"s_waitcnt lgkmcnt({len(issued) - 1 - last})")
         L.append(mfma(s))
+        issued = issued[last + 1:]
+        if s >= 30:  # next iteration's slots 0 and 1, into the entries MFMAs 30 and 31 read
+            L += read(s + 2)
+            issued += [s + 2] * 2
         L += slots[s]
     L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
     L += ["s_cmp_lg_u32 %[flag], 0", f"s_cbranch_scc1 L_oscale_{u}_%=", f"L_oscaled_{u}_%=:"]
@@ -440,6 +452,10 @@ def program_spread() -> list[str]:
          "s_mov_b32 %[krd], %[krd0]", "s_mov_b32 %[kwr], %[kwr0]", "s_nop 1"]
     # ---- S(1) = K(1) . Q^T: key block 0 into P region B, key block 1 into SB1 ----
     KB, KA = TX + 1, TX
+    # V(2) into V slot 2 (the loop copies V two epochs ahead)
+    L += [f"s_add_u32 m0, %[ldsw], {5 * TILE}", "s_nop 0", "global_load_lds_dwordx4 %[vo0], %[vb]",
+          f"s_add_u32 m0, %[ldsw], {5 * TILE + 8192}", "s_nop 0", "global_load_lds_dwordx4 %[vo1], %[vb]",
+          "v_add_u32 %[vo0], %[vt2], %[vo0]", "v_add_u32 %[vo1], %[vt2], %[vo1]"]
     L += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]
 
     def kread(f: int) -> list[str]:
@@ -458,11 +474,12 @@ def program_spread() -> list[str]:
         src_c = "0" if f & 7 == 0 else v(dst, 16)
         L.append(f"v_mfma_f32_32x32x16_f16 {v(dst, 16)}, {v(RING + 4 * (f % 3), 4)}, "
                  f"{v(Q + 4 * (f & 7), 4)}, {src_c}")
-    # K(2) and V(1), copied by the epoch before the loop, land for every wave; K(2) is next
-    L += ["s_waitcnt vmcnt(0)", "s_barrier",
+    # K(2) and V(1), copied by the epoch before the loop, land for every wave (V(2) may stay in
+    # flight); K(2) is next; the first two V(0) fragments of iteration 1
+    L += ["s_waitcnt vmcnt(2)", "s_barrier",
           "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
           "s_nop 7", "s_nop 7", "s_nop 7"]
-    L += block0_max(P[1])
+    L += block0_max(P[1]) + vread(0, 0) + vread(1, 0)
     L += ["L_epochs_%=:"]
     for u in range(4):
         L += spread_iteration(u)
@@ -472,7 +489,8 @@ def program_spread() -> list[str]:
         L += spread_out_of_line(u)
     # the compiled code after the statement reads O and reuses the score registers: MFMA
     # result latency first
-    L += ["L_done_%=:", "s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
+    # (and the last iteration's two V reads for an iteration that does not come have landed)
+    L += ["L_done_%=:", "s_waitcnt lgkmcnt(0)", "s_mov_b32 m0, %[msave]", "s_nop 7", "s_nop 7", "s_nop 7"]
     return L
 
 
