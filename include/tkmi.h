@@ -202,6 +202,17 @@ int tk_masked_softmax(const float *scores, tk_half *probs, int64_t groups,
  * 16-byte aligned.
  * scale: the attention scale (1/sqrt(unpadded head_dim)).  Dense inputs only
  * (no padding mask).  Shapes: tk_small_forward_supported.
+ * Causal sequences of more than 32 tokens run one 32-row block per
+ * workgroup when batch * ceil(seq/32) workgroups fit on the device's CUs at
+ * once and batch * layers * 4 <= 4096: the blocks of a sequence hand each
+ * layer's K and V rows to one another through a workspace the library
+ * allocates on the device the first time a call needs it (and replaces by a
+ * larger one, keeping the old, when a call needs more; 16 KB per sequence,
+ * layer and block, plus 16 KB), with
+ * the same results bit for bit as one workgroup per sequence.  Calls that
+ * overlap on one device share that workspace and must not run concurrently;
+ * a call made while its stream is being captured into a graph, with no
+ * workspace yet large enough, runs one workgroup per sequence instead.
  * Replaces the layer loop of OptimizedTransformer._run_layers_fused
  * (src/optimized.py:488-554) for the narrow configs (reference config 1 and
  * the appendix cases of src/configs/shapes.json with d_model 128).

@@ -271,9 +271,11 @@ def test_non_prefix_mask_parity(causal, fused):
     assert bool((got[~mask] == 0).all())
 
 
-# the layer path; the fused QKV + attention path (S = 64, head_dim 64)
-@pytest.mark.parametrize("shape", [(4, 64, 128, 4, 256, 2, True), (4, 64, 512, 8, 1024, 2, False)],
-                         ids=["layers", "fused_qkv_attention"])
+# the layer path; the fused QKV + attention path (S = 64, head_dim 64); the whole-forward
+# kernel with sequences split into 32-row blocks (causal, S = 128)
+@pytest.mark.parametrize("shape", [(4, 64, 128, 4, 256, 2, True), (4, 64, 512, 8, 1024, 2, False),
+                                   (8, 128, 128, 4, 128, 2, True)],
+                         ids=["layers", "fused_qkv_attention", "whole_forward_split"])
 def test_graphed_forward_replays_match_eager(shape):
     """Whole-forward HIP graph (src/cuda_graphs.py semantics): after the eager
     warm-up calls the graph is captured; every replay -- with eager work and

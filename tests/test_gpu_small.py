@@ -73,8 +73,9 @@ def test_small_forward_parity(shape):
 
 
 def test_small_forward_is_deterministic_and_batch_independent():
-    """Each sequence is one workgroup: a batch's outputs equal the outputs
-    of its sequences run alone, bit for bit, and reruns are identical."""
+    """A sequence's rows are computed the same way whatever else the batch
+    holds: a batch's outputs equal the outputs of its sequences run alone,
+    bit for bit, and reruns are identical."""
     _, opt = _pair((4, 96, 128, 4, 128, 2, True))
     x = torch.randn(4, 96, 128, generator=torch.Generator().manual_seed(3)).to(DEV)
     with torch.inference_mode():
@@ -105,3 +106,33 @@ def test_padded_input_takes_the_layer_path():
     keep = mask[..., None].expand_as(ref)
     res = ob.compare_outputs(ref[keep], got.cpu()[keep])
     assert res.passed, res.max_abs_error
+
+
+@pytest.mark.parametrize("s,h", [(128, 4), (96, 1), (64, 8), (50, 2)])
+def test_split_sequences_match_whole_sequence_workgroups(s, h):
+    """Causal shapes with more than one 32-row block run one block per
+    workgroup (K/V handed between the blocks of a sequence through the
+    library's workspace) when every workgroup of the launch fits on the CUs
+    at once, and one workgroup per sequence otherwise.  The same sequences
+    through both launches agree bit for bit (each row's arithmetic is the
+    same), and pass the oracle; a repeat of the split launch (its hand-off
+    counts left at zero by the first) is identical."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    mb = (s + 31) // 32
+    n_split = max(1, min(cus // mb, 64))
+    n_whole = cus // mb + 1  # too many workgroups to split
+    shape = (n_whole, s, 128, h, 128, 2, True)
+    base, opt = _pair(shape, seed=77 + s)
+    x = torch.randn(n_whole, s, 128, generator=torch.Generator().manual_seed(11 + s))
+    with torch.inference_mode():
+        whole = opt(x.to(DEV))
+        split = opt(x[:n_split].to(DEV))
+        again = opt(x[:n_split].to(DEV))
+    assert torch.equal(split, again)
+    assert torch.equal(split, whole[:n_split])
+    with torch.no_grad():
+        ref = base(x[:n_split])
+    res = ob.compare_outputs(ref, split.cpu())
+    print(f"s={s} h={h}: split batch {n_split}, whole-sequence batch {n_whole}, max_abs={res.max_abs_error:.3g}",
+          flush=True)
+    assert res.passed, (res.max_abs_error, res.failed_elements)

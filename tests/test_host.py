@@ -213,8 +213,9 @@ BENCH_ATTENTION = [("flash_fwd_kernel", 32, 4, 1), ("flash_single_kernel", 64, 2
                    ("flash_fwd_kernel", 128, 8, 1)]
 
 
-# The whole-forward kernel instantiation C1 runs (head_dim 32, causal).
-SMALL_FORWARD_C1 = "_ZN2tk12_GLOBAL__N_120small_forward_kernelILi128ELi128ELi128ELi32ELb1EEEvNS0_9SmallArgsE"
+# The whole-forward kernel instantiation C1 runs (head_dim 32, causal, sequences split into
+# 32-row blocks).
+SMALL_FORWARD_C1 = "_ZN2tk12_GLOBAL__N_120small_forward_kernelILi128ELi128ELi128ELi32ELb1ELb1EEEvNS0_9SmallArgsE"
 
 
 def test_hot_kernels_use_no_scratch():
@@ -243,7 +244,8 @@ def test_hot_kernels_use_no_scratch():
     assert any("flash_generic_kernelILi256E" in k and "ELb1EEEv" in k for k in hot)  # the head_dim-256 vector path
     hot.append(SMALL_FORWARD_C1)
     small = [k for k in usage if "small_forward_kernel" in k and k not in hot]
-    assert len(small) == 7  # head dims 16, 32, 64, 128, causal and not (C1's listed above)
+    # head dims 16, 32, 64, 128: causal and not, and causal split (C1's listed above)
+    assert len(small) == 11
     hot += small
     missing = [k for k in hot if k not in usage]
     assert not missing, missing

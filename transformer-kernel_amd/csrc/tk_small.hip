@@ -30,6 +30,9 @@
 // statistics, bias/GELU/residual in fp32 before each fp16 rounding.
 #include "tk_common.hpp"
 
+#include <algorithm>
+#include <mutex>
+
 namespace tk {
 namespace {
 
@@ -57,6 +60,11 @@ struct SmallArgs {
   float n1_eps, n2_eps, nf_eps;
   float scale_log2;  // attention scale * log2(e)
   int S, L, H;
+  // Split sequences (one 32-row block per workgroup): batch size, K/V hand-off slots
+  // [batch][layer][4 blocks][K rows | V rows] and their consumer counts, same index.
+  int B;
+  char* ws;
+  unsigned* flags;
 };
 
 // Byte offset of 16-byte chunk c of row r in an activation tile: the chunk
@@ -77,8 +85,22 @@ __device__ __forceinline__ void lds_sync() {
   asm volatile("" ::: "memory");
 }
 
-template <int D, int DP, int F, int HDP, bool CAUSAL>
+// Bound on a split block's wait for an earlier block's K/V (each try sleeps ~128 cycles): every
+// block of a split launch is resident (the host splits only when batch x blocks <= CUs) and the
+// earlier blocks of a sequence never wait on later ones, so it is never reached in a working
+// launch; if it is, the block's output rows are NaN instead of a hang.
+constexpr unsigned kSpinLimit = 1u << 20;
+constexpr int kSlotBytes = 2 * 32 * kPitch;  // K then V rows of one 32-row block: 16 KB
+
+// SPLIT (causal, S > 32): workgroup j * batch + b runs the 32-row block j of sequence b with 4
+// waves; after each layer's QKV it hands its K and V rows to the later blocks of the sequence
+// through p.ws and takes those of the earlier blocks (causal attention needs keys <= its rows
+// only).  Every other phase is row-local.  The ids are j-major, so the blocks a workgroup waits
+// for were dispatched before it, and with a batch that is a multiple of 8 a sequence's blocks
+// share an XCD (ids are dealt round-robin over the 8 XCDs) and its L2.
+template <int D, int DP, int F, int HDP, bool CAUSAL, bool SPLIT>
 __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
+  static_assert(!SPLIT || CAUSAL, "split sequences: causal attention only");
   static_assert(D == 128 && DP == 128 && F == 128, "one width: 4 column waves x 32 columns");
   static_assert(HDP == 16 || HDP == 32 || HDP == 64 || HDP == 128, "head dims with an MFMA k-step");
   constexpr int KD = D / 16, KP = DP / 16, KF = F / 16;  // k-steps
@@ -92,13 +114,14 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
                 V_N2W = V_N1B + D, V_N2B = V_N2W + D, VEC = V_N2B + D;
   static_assert(3 * DP <= 512, "b_qkv: at most two elements per thread of 256");
 
-  __shared__ __attribute__((aligned(16))) char smem[4 * kTile + 2 * 4 * kMaxRows * 4 + (2 * VEC + 2 * D) * 4];
+  __shared__ __attribute__((aligned(16))) char smem[4 * kTile + 2 * 4 * kMaxRows * 4 + (2 * VEC + 2 * D) * 4 + 16];
   char* Ht = smem;                // h (LayerNorm output) / ctx
   char* Qt = smem + kTile;        // Q / u
   char* Kt = smem + 2 * kTile;    // K
   char* Vt = smem + 3 * kTile;    // V
   float* stats = reinterpret_cast<float*>(smem + 4 * kTile);  // [2][4 column waves][128 rows]
   float* vecs = stats + 2 * 4 * kMaxRows;                     // [2][VEC], then nf_w, nf_b
+  int* lost = reinterpret_cast<int*>(vecs + 2 * VEC + 2 * D);  // split: an earlier block was not seen
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -114,7 +137,10 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
   auto refresh = [&]() { asm volatile("" : "+v"(g), "+v"(rl), "+v"(tq), "+v"(ts)); };
   const int S = p.S;
   const int MB = (S + 31) >> 5;
-  const int64_t b = blockIdx.x;
+  const int jb = SPLIT ? (int)(blockIdx.x / (unsigned)p.B) : 0;  // split: this workgroup's row block
+  const int64_t b = SPLIT ? (int64_t)(blockIdx.x % (unsigned)p.B) : (int64_t)blockIdx.x;
+  // row block of residual slot i (split: one slot, block jb)
+  auto mb_of = [&](int i) { return SPLIT ? jb : rh + 2 * i; };
   const float* xb = p.x + b * (int64_t)S * D;
   float* ob = p.out + b * (int64_t)S * D;
 
@@ -122,7 +148,7 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
   f32x16 xr[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int m = (rh + 2 * i) * 32 + rl;
+    const int m = mb_of(i) * 32 + rl;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
@@ -154,16 +180,18 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
     float mean[2], rstd[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+      if (SPLIT && i > 0) break;
       float s = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s += xr[i][r];
       s = pair_sum(s);
-      if (g == 0) stats[wc * kMaxRows + (rh + 2 * i) * 32 + rl] = s;
+      if (g == 0) stats[wc * kMaxRows + mb_of(i) * 32 + rl] = s;
     }
     lds_sync();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int m = (rh + 2 * i) * 32 + rl;
+      if (SPLIT && i > 0) break;
+      const int m = mb_of(i) * 32 + rl;
       mean[i] = (stats[m] + stats[kMaxRows + m] + stats[2 * kMaxRows + m] + stats[3 * kMaxRows + m]) / (float)D;
       float s = 0.f;
 #pragma unroll
@@ -177,7 +205,8 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
     lds_sync();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int m = (rh + 2 * i) * 32 + rl;
+      if (SPLIT && i > 0) break;
+      const int m = mb_of(i) * 32 + rl;
       const float* s2 = stats + 4 * kMaxRows;
       const float var = (s2[m] + s2[kMaxRows + m] + s2[2 * kMaxRows + m] + s2[3 * kMaxRows + m]) / (float)D;
       rstd[i] = 1.0f / sqrtf(var + eps);
@@ -189,11 +218,13 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       const f32x4 bv = *reinterpret_cast<const f32x4*>(gb + n);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int m = (rh + 2 * i) * 32 + rl;
+        if (SPLIT && i > 0) break;
+        const int m = mb_of(i) * 32 + rl;
         float y[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = (xr[i][4 * q + e] - mean[i]) * rstd[i] * wv[e] + bv[e];
         if constexpr (FINAL) {
+          if (SPLIT && *lost) y[0] = y[1] = y[2] = y[3] = __builtin_nanf("");
           if (m < S) *reinterpret_cast<f32x4*>(ob + (int64_t)m * D + n) = f32x4{y[0], y[1], y[2], y[3]};
         } else {
           store_h4(Ht, m, n, y);
@@ -260,18 +291,87 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       v[V_N2B + tid] = vreg[7];
     }
   };
+  // Split: K/V hand-off of layer l (after its QKV phase).  This block's K and V rows go to its
+  // slot as they sit in its LDS tiles (the tiles' swizzle depends on the row only); once every
+  // wave's stores have completed, its count of consumers (the later blocks) is published; an
+  // earlier block's rows are read once its count is seen non-zero, and the count is decremented
+  // when they are in LDS, so every count is back at 0 when the launch ends.
+  // Ordering: the rows and the counts move only with agent-scope coherent accesses (sc1: what
+  // the compiler emits for relaxed agent-scope atomics, each location coherent across the
+  // device).  A producer's row stores have completed (vmcnt(0), every wave, then the barrier)
+  // before its count is stored; a consumer issues its row loads after it has read the count.
+  // So a consumer that sees the count reads the rows, without the release / acquire fences'
+  // L2 write-back and invalidate (18 us of a 73 us C1 forward).
+  auto exchange_kv = [&](int l) {
+    const int64_t slot0 = ((int64_t)b * p.L + l) * 4;
+    constexpr int kChunks = kSlotBytes / 16, kHalf = kChunks / 2;
+    if (jb + 1 < MB) {
+      char* dst = p.ws + (slot0 + jb) * kSlotBytes;
+      for (int c = tid; c < kChunks; c += (int)blockDim.x) {
+        const int half = c >= kHalf, off = (c - half * kHalf) * 16;
+        const f32x4 v = *reinterpret_cast<const f32x4*>((half ? Vt : Kt) + jb * 32 * kPitch + off);
+        asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst + half * (kSlotBytes / 2) + off), "v"(v)
+                     : "memory");
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      if (tid == 0)
+        __hip_atomic_store(p.flags + slot0 + jb, (unsigned)(MB - 1 - jb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (jb > 0) {
+      if (tid < jb) {
+        unsigned tries = 0;
+        while (__hip_atomic_load(p.flags + slot0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
+               ++tries < kSpinLimit)
+          __builtin_amdgcn_s_sleep(2);
+        if (tries >= kSpinLimit) *lost = 1;  // (its count is not decremented below)
+      }
+      __builtin_amdgcn_s_barrier();
+      static_assert(kChunks == 4 * 256, "four 16-byte chunks per thread of a 256-thread workgroup");
+      for (int blk = 0; blk < jb; ++blk) {
+        const char* src = p.ws + (slot0 + blk) * kSlotBytes;
+        const char* a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = tid + 256 * u, half = c >= kHalf;
+          a[u] = src + half * (kSlotBytes / 2) + (c - half * kHalf) * 16;
+        }
+        // loads and their wait in one statement: the outputs are complete when it ends
+        f32x4 v0, v1, v2, v3;
+        asm volatile(
+            "global_load_dwordx4 %0, %4, off sc1\n\t"
+            "global_load_dwordx4 %1, %5, off sc1\n\t"
+            "global_load_dwordx4 %2, %6, off sc1\n\t"
+            "global_load_dwordx4 %3, %7, off sc1\n\t"
+            "s_waitcnt vmcnt(0)"
+            : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+            : "memory");
+        const f32x4 vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = tid + 256 * u, half = c >= kHalf, off = (c - half * kHalf) * 16;
+          *reinterpret_cast<f32x4*>((half ? Vt : Kt) + blk * 32 * kPitch + off) = vv[u];
+        }
+      }
+      lds_sync();
+      if (tid < jb && !*lost)
+        __hip_atomic_fetch_add(p.flags + slot0 + tid, ~0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   vec_load(0);
   vec_store(0);
   if (threadIdx.x < D) {
     vecs[2 * VEC + threadIdx.x] = p.nf_w[threadIdx.x];
     vecs[2 * VEC + D + threadIdx.x] = p.nf_b[threadIdx.x];
   }
+  if (threadIdx.x == 0) *lost = 0;
   load_wq(0, 0);
   lds_sync();  // vectors of layer 0 and the final norm staged
   layer_norm(vecs + V_N1W, vecs + V_N1B, p.n1_eps, std::false_type{});
   // Attention work items: (head, 32-row query block), heaviest first (causal
   // cost grows with the block index), dealt to the NWV waves in snake order.
-  const int items = p.H * MB;
+  const int items = SPLIT ? p.H : p.H * MB;
   const int NWV = blockDim.x >> 6;
   for (int l = 0; l < p.L; ++l) {
     lds_sync();  // h complete
@@ -284,8 +384,9 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
         if (j + 1 < NQ) load_wq(l, j + 1);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          const int mb = rh + 2 * i;
-          if (mb >= MB) break;
+          if (SPLIT && i > 0) break;
+          const int mb = mb_of(i);
+          if (!SPLIT && mb >= MB) break;
           f32x16 acc = {};
 #pragma unroll
           for (int kk = 0; kk < KD; ++kk)
@@ -315,12 +416,13 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
     if constexpr (HDP < 128) load_wo(l);
     if (l + 1 < p.L) vec_load(l + 1);
     lds_sync();  // Q, K, V complete
+    if constexpr (SPLIT) exchange_kv(l);
     // ---- attention over this wave's (head, query block) items; ctx -> h tile ----
     for (int k = 0; k < items; ++k) {
       refresh();
       const int kr = k % (2 * NWV);
       if ((kr < NWV ? kr : 2 * NWV - 1 - kr) != w) continue;
-      const int qb = MB - 1 - k / p.H;
+      const int qb = SPLIT ? jb : MB - 1 - k / p.H;
       const int hh = k % p.H;
       const int hc = hh * HDP / 8;  // first chunk of this head's columns
       const int row = qb * 32 + rl;
@@ -425,8 +527,9 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       const f32x4* bo4 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_BO + 32 * wc + 4 * g);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int mb = rh + 2 * i;
-        if (mb >= MB) break;
+        if (SPLIT && i > 0) break;
+        const int mb = mb_of(i);
+        if (!SPLIT && mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
         for (int kk = 0; kk < KP; ++kk)
@@ -448,8 +551,9 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       const f32x4* b14 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B1 + 32 * wc + 4 * g);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int mb = rh + 2 * i;
-        if (mb >= MB) break;
+        if (SPLIT && i > 0) break;
+        const int mb = mb_of(i);
+        if (!SPLIT && mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk)
@@ -473,8 +577,9 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
       const f32x4* b24 = reinterpret_cast<const f32x4*>(vecs + (l & 1) * VEC + V_B2 + 32 * wc + 4 * g);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int mb = rh + 2 * i;
-        if (mb >= MB) break;
+        if (SPLIT && i > 0) break;
+        const int mb = mb_of(i);
+        if (!SPLIT && mb >= MB) break;
         f32x16 acc = {};
 #pragma unroll
         for (int kk = 0; kk < KF; ++kk)
@@ -497,11 +602,76 @@ __global__ __launch_bounds__(512, 1) void small_forward_kernel(SmallArgs p) {
 
 template <int HDP, bool CAUSAL>
 int launch_small(const SmallArgs& p, int64_t batch, hipStream_t st) {
+  if constexpr (CAUSAL) {
+    if (p.ws != nullptr) {  // split: one 32-row block per workgroup, 4 waves
+      const unsigned blocks = (unsigned)batch * (unsigned)((p.S + 31) / 32);
+      hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, true, true>), dim3(blocks), dim3(256), 0, st, p);
+      return check_launch("tk_small_forward");
+    }
+  }
   // 8 waves: column block w & 3, row blocks (w >> 2) + {0, 2}.  A single row
   // block (S <= 32) leaves waves 4-7 without rows: 4 waves then.
   const unsigned threads = p.S <= 32 ? 256 : 512;
-  hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, CAUSAL>), dim3((unsigned)batch), dim3(threads), 0, st, p);
+  hipLaunchKernelGGL((small_forward_kernel<128, 128, 128, HDP, CAUSAL, false>), dim3((unsigned)batch), dim3(threads),
+                     0, st, p);
   return check_launch("tk_small_forward");
+}
+
+// Compute units of the current device (cached per device).
+int device_cus(int dev) {
+  static int cus[64] = {0};
+  if (dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 1;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The split launch's hand-off workspace: a table of kMaxSlots consumer counts at a fixed place
+// (its start), then 4 block slots of K and V rows per (sequence, layer) -- count i belongs to
+// slot i.  Every launch leaves the counts it used at 0 and slots never overlap the table, so the
+// counts are 0 at every launch's start whatever shapes the workspace served before.
+constexpr int64_t kMaxSlots = 4096;                  // batch x layers x 4 (C1: 1024)
+constexpr int64_t kCountBytes = kMaxSlots * 4;
+int64_t split_ws_bytes(int64_t batch, int64_t layers) { return kCountBytes + batch * layers * 4 * kSlotBytes; }
+
+// Whether a shape runs split (one 32-row block per workgroup): causal, more than one row block,
+// every workgroup resident at once (batch x blocks <= CUs; a waiting block's producers then run).
+bool use_split(int64_t batch, int64_t seq, int64_t layers, bool causal, int dev) {
+  const int64_t mb = (seq + 31) / 32;
+  return causal && mb > 1 && batch * mb <= device_cus(dev) && batch * layers * 4 <= kMaxSlots;
+}
+
+// The split launch's workspace: one zeroed buffer per device, replaced by one at least twice as
+// large when a call needs more; kernels leave every consumer count at 0.  An outgrown buffer is
+// kept, not freed (a captured graph may still launch with it), so the device holds at most about
+// twice the largest workspace.  Never allocated while the stream is being captured (the call then
+// runs unsplit).
+std::mutex g_ws_mutex;
+struct Workspace {
+  char* ptr = nullptr;
+  int64_t bytes = 0;
+};
+Workspace g_ws[64];
+
+char* split_workspace(int dev, int64_t bytes, hipStream_t st) {
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  Workspace& w = g_ws[dev];
+  if (w.bytes >= bytes) return w.ptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  const int64_t want = std::max(bytes, 2 * w.bytes);
+  char* ptr = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&ptr), (size_t)want) != hipSuccess) return nullptr;
+  if (hipMemsetAsync(ptr, 0, (size_t)want, st) != hipSuccess) {
+    (void)hipFree(ptr);
+    return nullptr;
+  }
+  w.ptr = ptr;
+  w.bytes = want;
+  return ptr;
 }
 
 }  // namespace
@@ -566,6 +736,18 @@ extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64
   p.H = (int)heads;
   hipStream_t st = as_stream(stream);
   const bool c = causal != 0;
+  p.B = (int)batch;
+  p.ws = nullptr;
+  p.flags = nullptr;
+  int dev = 0;
+  TK_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, TK_ERR_HIP, "tk_small_forward: no device");
+  if (use_split(batch, seq, layers, c, dev)) {
+    char* ws = split_workspace(dev, split_ws_bytes(batch, layers), st);
+    if (ws != nullptr) {
+      p.flags = reinterpret_cast<unsigned*>(ws);
+      p.ws = ws + kCountBytes;
+    }
+  }
   switch (head_dim_padded) {
     case 16: return c ? launch_small<16, true>(p, batch, st) : launch_small<16, false>(p, batch, st);
     case 32: return c ? launch_small<32, true>(p, batch, st) : launch_small<32, false>(p, batch, st);
