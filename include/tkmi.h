@@ -229,6 +229,32 @@ int tk_small_forward(const float *x, float *out, int64_t batch, int64_t seq,
                      const float *nf_w, const float *nf_b, float n1_eps,
                      float n2_eps, float nf_eps, float scale, void *stream);
 
+/* tk_small_forward without any allocation: the same arguments, work and
+ * results (bit for bit), but a split launch hands its K/V rows through a
+ * fixed per-device scratch array (16 MB + 16 KB, in the library's code
+ * object: each device holds it from the library's load until the process
+ * ends) instead of the library's allocated workspace, and its count table is
+ * cleared by a small kernel at each call.  Returns TK_ERR_UNSUPPORTED when a
+ * split launch would need more than 1024 hand-off slots (batch * layers * 4
+ * row blocks, e.g. C1's B64 L4); shapes that run unsplit use no scratch.
+ * Calls that overlap on one device share that device's array and race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int tk_small_forward_noalloc(const float *x, float *out, int64_t batch,
+                             int64_t seq, int64_t d_model, int64_t heads,
+                             int64_t head_dim_padded, int64_t ffn_dim,
+                             int64_t layers, int causal, const tk_half *w_qkv,
+                             const float *b_qkv, const tk_half *w_o,
+                             const float *b_o, const tk_half *w_1,
+                             const float *b_1, const tk_half *w_2,
+                             const float *b_2, const float *n1_w,
+                             const float *n1_b, const float *n2_w,
+                             const float *n2_b, const float *nf_w,
+                             const float *nf_b, float n1_eps, float n2_eps,
+                             float nf_eps, float scale, void *stream);
+
 /* Fused QKV projection + attention for one-key-tile sequences:
  *   ctx[t, h*64 + :64] = attention_h( h . W_qkv^T + b_qkv )
  * i.e. tk_gemm(h, w_qkv, b_qkv) into a [T, 3*d_model] q|k|v buffer followed

@@ -686,29 +686,55 @@ extern "C" int tk_small_forward_supported(int64_t seq, int64_t d_model, int64_t 
          (hp == 16 || hp == 32 || hp == 64 || hp == 128) && heads * hp == 128;
 }
 
-extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64_t seq, int64_t d_model,
-                                int64_t heads, int64_t head_dim_padded, int64_t ffn_dim, int64_t layers, int causal,
-                                const tk_half* w_qkv, const float* b_qkv, const tk_half* w_o, const float* b_o,
-                                const tk_half* w_1, const float* b_1, const tk_half* w_2, const float* b_2,
-                                const float* n1_w, const float* n1_b, const float* n2_w, const float* n2_b,
-                                const float* nf_w, const float* nf_b, float n1_eps, float n2_eps, float nf_eps,
-                                float scale, void* stream) {
+// Scratch of tk_small_forward_noalloc (the split launch's count table and hand-off slots): a
+// fixed array of every device, located per device once with hipGetSymbolAddress.
+constexpr int64_t kNoAllocSlots = 1024;  // batch x layers x 4 blocks (C1: 1024)
+static __device__ __attribute__((aligned(256))) char scratch[kCountBytes + kNoAllocSlots * kSlotBytes];
+
+namespace {
+
+std::mutex g_scratch_mutex;
+char* g_scratch[64];
+
+// Device address of this device's scratch (the device current), or nullptr.
+char* scratch_address(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+    g_scratch[dev] = static_cast<char*>(ptr);
+  }
+  return g_scratch[dev];
+}
+
+__global__ void clear_counts(unsigned* counts, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) counts[i] = 0u;
+}
+
+int small_forward_call(const char* fn, bool noalloc, const float* x, float* out, int64_t batch, int64_t seq,
+                       int64_t d_model, int64_t heads, int64_t head_dim_padded, int64_t ffn_dim, int64_t layers,
+                       int causal, const tk_half* w_qkv, const float* b_qkv, const tk_half* w_o, const float* b_o,
+                       const tk_half* w_1, const float* b_1, const tk_half* w_2, const float* b_2, const float* n1_w,
+                       const float* n1_b, const float* n2_w, const float* n2_b, const float* nf_w,
+                       const float* nf_b, float n1_eps, float n2_eps, float nf_eps, float scale, void* stream) {
   clear_error();
   TK_REQUIRE(x && out && w_qkv && b_qkv && w_o && b_o && w_1 && b_1 && w_2 && b_2 && n1_w && n1_b && n2_w &&
                  n2_b && nf_w && nf_b,
-             TK_ERR_ARG, "tk_small_forward: null pointer");
+             TK_ERR_ARG, "%s: null pointer", fn);
   TK_REQUIRE(tk_small_forward_supported(seq, d_model, heads, head_dim_padded, ffn_dim), TK_ERR_UNSUPPORTED,
-             "tk_small_forward: shape S=%lld D=%lld H=%lld hd=%lld F=%lld outside the kernel's "
+             "%s: shape S=%lld D=%lld H=%lld hd=%lld F=%lld outside the kernel's "
              "(S <= 128, D = F = 128, H*hd = 128, hd in {16,32,64,128})",
-             (long long)seq, (long long)d_model, (long long)heads, (long long)head_dim_padded, (long long)ffn_dim);
+             fn, (long long)seq, (long long)d_model, (long long)heads, (long long)head_dim_padded,
+             (long long)ffn_dim);
   TK_REQUIRE(batch >= 0 && batch < (1ll << 31) && layers >= 1 && layers < (1 << 20), TK_ERR_ARG,
-             "tk_small_forward: batch=%lld layers=%lld", (long long)batch, (long long)layers);
-  TK_REQUIRE(scale > 0.f, TK_ERR_ARG, "tk_small_forward: scale must be > 0");
+             "%s: batch=%lld layers=%lld", fn, (long long)batch, (long long)layers);
+  TK_REQUIRE(scale > 0.f, TK_ERR_ARG, "%s: scale must be > 0", fn);
   auto al16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   TK_REQUIRE(al16(x) && al16(out) && al16(w_qkv) && al16(w_o) && al16(w_1) && al16(w_2) && al16(b_qkv) &&
                  al16(b_o) && al16(b_1) && al16(b_2) && al16(n1_w) && al16(n1_b) && al16(n2_w) && al16(n2_b) &&
                  al16(nf_w) && al16(nf_b),
-             TK_ERR_ARG, "tk_small_forward: every buffer must be 16-byte aligned");
+             TK_ERR_ARG, "%s: every buffer must be 16-byte aligned", fn);
   if (batch == 0) return TK_OK;
   SmallArgs p;
   p.x = x;
@@ -740,12 +766,28 @@ extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64
   p.ws = nullptr;
   p.flags = nullptr;
   int dev = 0;
-  TK_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, TK_ERR_HIP, "tk_small_forward: no device");
+  TK_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64, TK_ERR_HIP, "%s: no device", fn);
   if (use_split(batch, seq, layers, c, dev)) {
-    char* ws = split_workspace(dev, split_ws_bytes(batch, layers), st);
-    if (ws != nullptr) {
+    if (noalloc) {
+      // the device's static scratch: its count table is cleared first (a previous call on this
+      // device leaves it at 0 unless that call failed)
+      const int64_t slots = batch * layers * 4;
+      TK_REQUIRE(slots <= kNoAllocSlots, TK_ERR_UNSUPPORTED,
+                 "%s: batch %lld x layers %lld x 4 row blocks = %lld hand-off slots, more than the %lld of the "
+                 "static scratch (16 MB); use tk_small_forward",
+                 fn, (long long)batch, (long long)layers, (long long)slots, (long long)kNoAllocSlots);
+      char* ws = scratch_address(dev);
+      TK_REQUIRE(ws != nullptr, TK_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed", fn);
+      hipLaunchKernelGGL(clear_counts, dim3((unsigned)(kMaxSlots / 256)), dim3(256), 0, st,
+                         reinterpret_cast<unsigned*>(ws), (int)kMaxSlots);
       p.flags = reinterpret_cast<unsigned*>(ws);
       p.ws = ws + kCountBytes;
+    } else {
+      char* ws = split_workspace(dev, split_ws_bytes(batch, layers), st);
+      if (ws != nullptr) {
+        p.flags = reinterpret_cast<unsigned*>(ws);
+        p.ws = ws + kCountBytes;
+      }
     }
   }
   switch (head_dim_padded) {
@@ -754,4 +796,30 @@ extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64
     case 64: return c ? launch_small<64, true>(p, batch, st) : launch_small<64, false>(p, batch, st);
     default: return c ? launch_small<128, true>(p, batch, st) : launch_small<128, false>(p, batch, st);
   }
+}
+
+}  // namespace
+
+extern "C" int tk_small_forward(const float* x, float* out, int64_t batch, int64_t seq, int64_t d_model,
+                                int64_t heads, int64_t head_dim_padded, int64_t ffn_dim, int64_t layers, int causal,
+                                const tk_half* w_qkv, const float* b_qkv, const tk_half* w_o, const float* b_o,
+                                const tk_half* w_1, const float* b_1, const tk_half* w_2, const float* b_2,
+                                const float* n1_w, const float* n1_b, const float* n2_w, const float* n2_b,
+                                const float* nf_w, const float* nf_b, float n1_eps, float n2_eps, float nf_eps,
+                                float scale, void* stream) {
+  return small_forward_call("tk_small_forward", false, x, out, batch, seq, d_model, heads, head_dim_padded, ffn_dim,
+                            layers, causal, w_qkv, b_qkv, w_o, b_o, w_1, b_1, w_2, b_2, n1_w, n1_b, n2_w, n2_b, nf_w,
+                            nf_b, n1_eps, n2_eps, nf_eps, scale, stream);
+}
+
+extern "C" int tk_small_forward_noalloc(const float* x, float* out, int64_t batch, int64_t seq, int64_t d_model,
+                                        int64_t heads, int64_t head_dim_padded, int64_t ffn_dim, int64_t layers,
+                                        int causal, const tk_half* w_qkv, const float* b_qkv, const tk_half* w_o,
+                                        const float* b_o, const tk_half* w_1, const float* b_1, const tk_half* w_2,
+                                        const float* b_2, const float* n1_w, const float* n1_b, const float* n2_w,
+                                        const float* n2_b, const float* nf_w, const float* nf_b, float n1_eps,
+                                        float n2_eps, float nf_eps, float scale, void* stream) {
+  return small_forward_call("tk_small_forward_noalloc", true, x, out, batch, seq, d_model, heads, head_dim_padded,
+                            ffn_dim, layers, causal, w_qkv, b_qkv, w_o, b_o, w_1, b_1, w_2, b_2, n1_w, n1_b, n2_w,
+                            n2_b, nf_w, nf_b, n1_eps, n2_eps, nf_eps, scale, stream);
 }

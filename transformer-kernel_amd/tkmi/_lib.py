@@ -66,6 +66,11 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int]
         + [c_void_p] * 14 + [c_float, c_float, c_float, c_float, c_void_p],
     ),
+    "tk_small_forward_noalloc": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int]
+        + [c_void_p] * 14 + [c_float, c_float, c_float, c_float, c_void_p],
+    ),
     "tk_small_forward_supported": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int64]),
 }
 
