@@ -33,10 +33,11 @@ gen = _gen("gen_attn_epochs")
 gen64 = _gen("gen_attn_steps64")
 class _G64:
     """A head_dim-64 loop variant through the common generator interface."""
-    CLOBBERED, PINNED = gen64.CLOBBERED, gen64.PINNED
+    PINNED = gen64.PINNED
 
     def __init__(self, nw, kmask):
         self.nw, self.kmask = nw, kmask
+        self.CLOBBERED = gen64.KMASK_CLOBBERED if kmask else gen64.CLOBBERED
 
     def program(self):
         return gen64.program(self.nw, self.kmask)
@@ -84,7 +85,7 @@ def test_kernel_clobber_list_matches_the_generator(loop):
         d = src.rindex(f"#define {name}", 0, i)
         stmt = src[d:src.index("if constexpr", d)] + stmt
     clobbers = [int(r) for r in re.findall(r'"v(\d+)"', stmt)]
-    assert clobbers == g.CLOBBERED
+    assert sorted(clobbers) == g.CLOBBERED and len(set(clobbers)) == len(clobbers)
     for extra in ('"vcc"', '"scc"', '"memory"'):
         assert extra in stmt
 
@@ -316,16 +317,70 @@ def test_spread_loop_reads_each_score_before_it_is_replaced(u):
     assert [sorted(x.reads - {f"v{gen.LS}"}) for x in dots] == [[f"v{X + j}"] for j in range(16)]
 
 
+def _hd64_refits(prog):
+    """Split the dense head_dim-64 loop into its main path and its refit blocks (the
+    instructions between the overflow branch and its L_fits label)."""
+    main, refits, cur = [], [], None
+    for l in prog:
+        if l.startswith("s_cbranch_vccz L_fits_"):
+            main.append(l)
+            cur = []
+        elif cur is not None and l.startswith("L_fits_"):
+            refits.append(cur)
+            main.append(l)
+            cur = None
+        elif cur is not None:
+            cur.append(l)
+        else:
+            main.append(l)
+    return main, refits
+
+
 def test_hd64_loop_covers_two_steps_of_16_mfmas():
     prog = gen64.program()
+    main, refits = _hd64_refits(prog)
     assert sum(1 for l in prog if l.startswith("v_mfma")) == 2 * 16
+    assert not any(l.startswith("v_mfma") for r in refits for l in r)
     assert sum(1 for l in prog if l == "s_barrier") == 2
     assert sum(1 for l in prog if l.startswith("global_load_lds")) == 2 * 4
     # 32 exponentials and 16 packs per step, every row-sum term in order
     temps = tuple(f"v_exp_f32 v{r}," for r in (gen64.T0, gen64.T1, gen64.T2, gen64.T3))
-    assert sum(1 for l in prog if l.startswith(temps)) == 2 * 32
-    dots = [l for l in prog if l.startswith("v_dot2c")]
+    assert sum(1 for l in main if l.startswith(temps)) == 2 * 32
+    dots = [l for l in main if l.startswith("v_dot2c")]
     assert len(dots) == 32
+    # no row max on the main path: the rescale runs only when a P entry overflows fp16
+    assert not any(l.startswith(("v_max", "v_permlane")) for l in main)
+
+
+def test_hd64_refit_recomputes_p_as_the_step_does():
+    """When some P(kt) entry overflows fp16 (its row sum is inf or NaN), the dense step
+    takes the row max of S(kt), rescales l and O to m_new = max(m_run, m_tile) and computes
+    P(kt) and its row sum again: the same scale, exponential, pack and dot operations on
+    the same registers, in the same order, as the step's slots."""
+    prog = gen64.program()
+    main, refits = _hd64_refits(prog)
+    assert len(refits) == 2
+    p_ops = ("v_fma_f32", "v_exp_f32", "v_cvt_pk_f16_f32", "v_dot2c_f32_f16")
+    steps = [[], []]
+    k = 0
+    for l in main:
+        if l.startswith("s_cbranch_vccz L_fits_"):
+            k += 1
+        elif k < 2 and l.startswith(p_ops):
+            steps[k].append(l)
+    for par in (0, 1):
+        r = refits[par]
+        s_cur = gen64.X if par == 0 else gen64.Y
+        maxes = [l for l in r if l.startswith(("v_max3_f32", "v_max_f32 v212, v212, v1"))]
+        regs = sorted(int(x) for l in maxes for x in re.findall(r"v(\d+)", l)[1:] if int(x) != gen64.MX)
+        assert regs == list(range(s_cur, s_cur + 32))
+        reset = r.index(f"v_mov_b32 v{gen64.LS}, 0")
+        assert [l for l in r[reset:] if l.startswith(p_ops)] == steps[par]
+        assert r.index(f"v_mov_b32 v{gen64.MR}, v{gen64.TMP}") < reset
+        o_muls = [l for l in r if l.startswith("v_mul_f32 v") and int(l.split()[1][1:-1]) in range(64, 96)]
+        assert len(o_muls) == 32
+    # the overflow test reads the finished row sum: inf or NaN take the refit
+    assert sum(1 for l in main if l == f"v_cmp_ngt_f32 vcc, 0x7f800000, v{gen64.LS}") == 2
 
 
 def test_hd64_loops_differ_only_in_the_copies():
@@ -359,22 +414,24 @@ def test_key_masked_loop_adds_only_the_mask_work():
 
 @pytest.mark.parametrize("nw", [4, 8])
 def test_hd64_key_masked_loop_adds_only_the_mask_work(nw):
-    """The key-masked head_dim-64 loop keeps every instruction of the dense one in
-    order, except that the row max over a tile's scores moves from the step before
-    (into v160/v163, copied to T0 and T1) to after the selects that set masked
-    keys to -inf (straight into T0); it adds the byte load, key bits, the selects
-    and the m = -inf guard."""
-    dense, masked = gen64.program(nw, False), gen64.program(nw, True)
-    early = lambda l: l.startswith(("v_max3_f32 v160", "v_max_f32 v160", "v_max3_f32 v163", "v_max_f32 v163"))
-    late = lambda l: l.startswith(("v_max3_f32 v212", "v_max_f32 v212, v212, v1"))
-    copies = ("v_mov_b32 v212, v160", "v_mov_b32 v213, v160", "v_mov_b32 v212, v163", "v_mov_b32 v213, v163")
-    kept = [l for l in dense if not early(l) and l not in copies]
+    """The key-masked head_dim-64 loop keeps every instruction of the dense one's main path
+    in order; in place of the dense end-of-step overflow test it rescales at the start of
+    the step (the lazy test on the row max of the masked scores, O scaled at the step end),
+    and it adds the byte load, key bits, the selects and the m = -inf guard."""
+    dense, _ = _hd64_refits(gen64.program(nw, False))
+    masked = gen64.program(nw, True)
+    check = (f"v_cmp_ngt_f32 vcc, 0x7f800000, v{gen64.LS}", "s_nop 3")
+    kept = [l for l in dense if not l.startswith(("s_cbranch_vccz L_fits_", "L_fits_")) and l not in check]
     it = iter(masked)
     assert all(any(m == l for m in it) for l in kept)
-    assert not any(map(early, masked))
-    scores = lambda prog, sel: sorted(int(r) for l in prog if sel(l) for r in re.findall(r"v(\d+)", l)[1:]
-                                      if int(r) not in (160, 163, 212))
-    assert scores(dense, early) == scores(masked, late) == [*range(112, 144), *range(164, 196)]
+    extra = [l for l in masked if l not in kept]
+    assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "s_waitcnt vmcnt", "v_cmp_", "s_mov_b32 s9",
+                             "s_mov_b64 s[94:95]", "s_mov_b64 s[92:93], %[kbits]", "s_bfe_i32", "v_cndmask_b32", "v_mov_b32 v", "v_max",
+                             "v_permlane32_swap", "v_mul_f32", "v_add_f32 v213", "v_sub_f32", "v_exp_f32 v216",
+                             "s_nop", "s_cbranch_vccz L_norescale", "L_norescale", "s_mov_b32 %[flag]",
+                             "s_cmp_eq_u32 %[flag]", "s_cbranch_scc1 L_noscale", "L_noscale")) for l in extra), extra
+    maxes = [l for l in masked if l.startswith("v_max3_f32 v212")]
+    assert len(maxes) == 2 * 15
     assert sum(1 for l in masked if l.startswith("s_bfe_i32")) == 2 * 2 * 32
     src = (CSRC / "tk_attention.hip").read_text()
     i = src.index(f'#include "{gen64.INCS[(nw, True)]}"')

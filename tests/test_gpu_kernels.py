@@ -460,6 +460,46 @@ def test_flash_attention_large_logits(hd):
         assert bad == 0, (causal, err)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("slope", [6.0, 24.0])
+def test_flash_attention_scores_rising_along_keys(hd, slope):
+    """Scores that rise by `slope` (in log2 units) per 64-key tile along the keys, for every
+    query row: the running max must move on most tiles (24: every tile's exponentials
+    against the old reference overflow fp16, so the steps that rescale only on overflow
+    redo P on every tile; 6: every third tile or so).  Against the reference, and the
+    generated loops against the compiled steps bit for bit (K/V rows 4 MiB apart, as in
+    test_flash_attention_epoch_loop_is_bit_identical)."""
+    b, h, s = 1, 2, 1024
+    g = torch.Generator().manual_seed(int(slope) * 7 + hd)
+    u = torch.randn(hd, generator=g)
+    u = u / u.norm()
+    cs = hd ** -0.5 * 1.4426950408889634
+    # s_ij * cs = cs * (4 u + noise).(c t_j u + noise) ~ 4 c cs t_j: c for `slope` per tile
+    c = slope / (4.0 * cs)
+    t = torch.arange(s, dtype=torch.float32) / 64.0
+    q = (4.0 * u + 0.1 * torch.randn(b, h, s, hd, generator=g)).half()
+    k = (c * t[:, None] * u + torch.randn(b, h, s, hd, generator=g)).half()
+    v = torch.randn(b, h, s, hd, generator=g).half()
+    assert torch.isfinite(k).all()
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    for causal in (True, False):
+        out = ops.flash_attention(qd, kd, vd, hd ** -0.5, causal)
+        bad, err = or_rule_violations(out, ob.attention_ref(q, k, v, hd ** -0.5, causal))
+        assert bad == 0, (causal, err)
+    compact = ops.flash_attention(qd, kd, vd, hd ** -0.5, True)
+    rs = 1 << 21
+    wide_k = torch.zeros(b * h * s, rs, dtype=torch.float16, device=DEV)
+    wide_v = torch.zeros(b * h * s, rs, dtype=torch.float16, device=DEV)
+    wide_k[:, :hd] = kd.reshape(-1, hd)
+    wide_v[:, :hd] = vd.reshape(-1, hd)
+    kw = wide_k.view(b, h, s, rs)[..., :hd]
+    vw = wide_v.view(b, h, s, rs)[..., :hd]
+    assert kw.stride(2) == rs and torch.equal(kw, kd)
+    spread = ops.flash_attention(qd, kw, vw, hd ** -0.5, True)
+    del wide_k, wide_v
+    assert torch.equal(compact, spread)
+
+
 def _attention_ref_keymask(q, k, v, scale, causal, key_valid):
     """Baseline order (src/torch_transformer_benchmark.py:97-112) with the key mask of :105-108."""
     scores = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale

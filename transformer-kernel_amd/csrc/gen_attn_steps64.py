@@ -10,16 +10,22 @@ What a step computes
 --------------------
 Step kt of the DMA body (key tile kt = keys 64kt .. 64kt+63), for every wave:
 
-  max       m_tile = scale*log2(e) * (row max of S(kt) over the lane pair, found during the
-            previous step); lazy rescale when any lane's m_tile exceeds m_run + 8:
-            m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new), l_run *= alpha
   16 slots  slot m < 8: S^T(kt+1) MFMA m (key block m / 4, k-step m % 4);
             slot m >= 8: O^T += V^T(kt-1) . P^T(kt-1), MFMA m - 8 (head-dim block (m-8) % 2,
             P block (m-8) / 2); exponential pair m of S(kt) (entries 2m, 2m+1) between the
-            MFMAs -> P(kt), fp16 row sum with v_dot2c; row max of S(kt+1) once its MFMAs are done
+            MFMAs -> P(kt) = exp2(cs*S(kt) - m_run), fp16 row sum with v_dot2c
   copies    K tile kt+2 after slot 0, V tile kt+1 after slot 2 (LDS DMA)
-  end       l_run += row sum; O *= alpha when the rescale ran; wait for this step's copies;
-            barrier
+  fit       the reference m_run moves only when some P(kt) entry overflows fp16 (>= 2^16: the
+            row sum is then inf; a NaN score also lands here): then m_tile = cs * (row max of
+            S(kt) over the lane pair), m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new),
+            l_run *= alpha, O *= alpha (O holds tiles < kt), and P(kt) and its row sum again
+  end       l_run += row sum; wait for this step's copies; barrier
+
+No row max is taken on the common path (the max chain and the rescale test were ~20 of a step's
+~130 VALU instructions; the step is VALU-bound).  Exponentials up to 2^16 keep fp16's relative
+precision, and O, l accumulate in fp32, so a reference up to 16 below the row max costs nothing.
+The key-masked loops keep the lazy test at the step start (rescale when any lane's m_tile, from
+the masked scores, exceeds m_run + 8; O *= alpha at the step end), since m_run may still be -inf.
 
 Each lane performs the compiled step's operations on the same operands in the same order (the
 MFMA accumulation chains, the exponentials, the fp16 packing and the row-sum order; the row max
@@ -31,9 +37,9 @@ applies in these steps), so m_run and m_tile are -inf for all rows of a wave or 
 wave-wide rescale test never fires for a row whose m_new would be -inf.  The rescale still maps
 m_new = -inf to alpha = 1 (one compare and one select on that rare path), so l and O cannot turn
 into NaN if the loop's gate ever admits rows with different key histories.  Two steps per
-iteration: the score, P and
-max registers swap roles between them (the compiled loop's s_a/s_b, pf_a/pf_b, mx_a/mx_b), the
-K slot (2 slots) follows the parity and the V slots (3) rotate through SGPR trackers.
+iteration: the score and P registers swap roles between them (the compiled loop's s_a/s_b,
+pf_a/pf_b), the K slot (2 slots) follows the parity and the V slots (3) rotate through SGPR
+trackers.
 
 Register map (VGPRs; the asm statement pins or clobbers every one of them)
 --------------------------------------------------------------------------
@@ -41,9 +47,9 @@ Register map (VGPRs; the asm statement pins or clobbers every one of them)
   v[96:111]   Q fragments, 4 x 4                            (in)
   v[112:143]  scores X: S(kt) at entry and exit             (in/out)
   v[144:159]  P tile W: P(kt-1) at entry and exit           (in/out)
-  v160        row max of X's scores                         (in/out)
+  v160        key-masked: validity bytes of the next tile   (in/out; unused without a mask)
   v161, v162  m_run, l_run                                  (in/out)
-  v163        row max of Y's scores                         (clobbered)
+  v163        key-masked: validity bytes (other parity)     (clobbered by the key-masked loops)
   v[164:195]  scores Y                                      (clobbered)
   v[196:211]  P tile Z                                      (clobbered)
   v212..v217  temporaries                                   (clobbered)
@@ -74,11 +80,49 @@ TILE = 8192                           # bytes per K or V tile (64 rows x 128 byt
 KSLOTS, VSLOTS = 2, 3
 
 PINNED = set(range(64, 160)) | {MXX, MR, LR}
-CLOBBERED = sorted({MXY} | set(range(164, 230)))
+CLOBBERED = list(range(164, 230))
+KMASK_CLOBBERED = sorted({MXY} | set(CLOBBERED))   # v163: the next tile's validity bytes
 
 
 def v(a: int, n: int = 1) -> str:
     return f"v{a}" if n == 1 else f"v[{a}:{a + n - 1}]"
+
+
+def row_max(s: int) -> list[str]:
+    """Row max of the 32 scores s[0:32] of this lane, then over the lane pair, times cs: MX =
+    m_tile (TMP clobbered)."""
+    L = [f"v_max3_f32 {v(MX)}, {v(s)}, {v(s + 1)}, {v(s + 2)}"]
+    for k in range(3, 31, 2):
+        L.append(f"v_max3_f32 {v(MX)}, {v(MX)}, {v(s + k)}, {v(s + k + 1)}")
+    return L + [f"v_max_f32 {v(MX)}, {v(MX)}, {v(s + 31)}", f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1",
+                f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
+                f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
+                f"v_mul_f32 {v(MX)}, {v(MX)}, %[cs]"]
+
+
+def rescale(tag: str, flag: str | None = None) -> list[str]:
+    """m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new) (1 for m_new = -inf), l_run *=
+    alpha.  With flag (the lazy test of the key-masked steps): only when some lane's m_tile
+    exceeds m_run + 8, and the flag asks for O *= alpha at the end of the step."""
+    L = []
+    if flag:
+        L += [f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",             # m_run + 8
+              f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
+              f"s_cbranch_vccz L_norescale_{tag}_%="]
+    L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",                     # m_new
+          f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
+          f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
+          f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",                    # m_new = -inf: alpha = 1
+          f"v_mov_b32 {v(MR)}, {v(TMP)}",
+          f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
+          f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}"]
+    if flag:
+        L += [flag, f"L_norescale_{tag}_%=:"]
+    return L
+
+
+def o_scale() -> list[str]:
+    return [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(32)]
 
 
 def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
@@ -93,38 +137,17 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
     rows with no valid key yet exponentiate against 0 and keep m = -inf."""
     s_cur, s_nxt = (X, Y) if par == 0 else (Y, X)
     p_prev, p_cur = (W, Z) if par == 0 else (Z, W)
-    mx_cur, mx_nxt = (MXX, MXY) if par == 0 else (MXY, MXX)
+    kb_nxt = MXY if par == 0 else MXX      # key-masked: the next tile's validity bytes
     k_rd = par * TILE                     # K(kt+1) is read from slot (kt + 1) % 2 = par
     k_wr = (1 - par) * TILE               # K(kt+2) is written into slot kt % 2
 
-    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    L = ["s_mov_b32 %[flag], 0"] if kmask else []
+    L += [f"v_mov_b32 {v(LS)}, 0"]
     if kmask:
-        L += [f"global_load_ubyte {v(mx_nxt)}, %[koff], %[kvb]", "v_add_u32 %[koff], 64, %[koff]"]
-    # ---- row max of S(kt) over the lane pair, lazy rescale ----
-    if kmask:
+        L += [f"global_load_ubyte {v(kb_nxt)}, %[koff], %[kvb]", "v_add_u32 %[koff], 64, %[koff]"]
+        # ---- row max of S(kt) after the mask, over the lane pair; lazy rescale ----
         L += key_mask(lambda i: s_cur + i, ALPHA)
-        L.append(f"v_max3_f32 {v(MX)}, {v(s_cur)}, {v(s_cur + 1)}, {v(s_cur + 2)}")
-        for k in range(3, 31, 2):
-            L.append(f"v_max3_f32 {v(MX)}, {v(MX)}, {v(s_cur + k)}, {v(s_cur + k + 1)}")
-        L += [f"v_max_f32 {v(MX)}, {v(MX)}, {v(s_cur + 31)}", f"v_mov_b32 {v(TMP)}, {v(MX)}"]
-    else:
-        L += [f"v_mov_b32 {v(TMP)}, {v(mx_cur)}", f"v_mov_b32 {v(MX)}, {v(mx_cur)}"]
-    L += ["s_nop 1",
-          f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
-          f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
-          f"v_mul_f32 {v(MX)}, {v(MX)}, %[cs]",                  # m_tile
-          f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",             # m_run + 8
-          f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
-          f"s_cbranch_vccz L_norescale_{par}_%="]
-    L += [f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",                # m_new
-          f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
-          f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
-          f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",               # m_new = -inf: alpha = 1
-          f"v_mov_b32 {v(MR)}, {v(TMP)}",
-          f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
-          f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
-          "s_mov_b32 %[flag], 1"]
-    L += [f"L_norescale_{par}_%=:"]
+        L += row_max(s_cur) + rescale(f"{par}", "s_mov_b32 %[flag], 1")
     if kmask:  # rows with no valid key so far: exponentials against 0, m_run restored after
         L += [f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(MR)}", f"s_mov_b64 s[{S_NOKEY}:{S_NOKEY + 1}], vcc",
               f"v_cndmask_b32 {v(MR)}, {v(MR)}, 0, vcc"]
@@ -167,24 +190,6 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
         return [f"v_cvt_pk_f16_f32 {v(p_cur + j)}, {v(a)}, {v(b)}",
                 f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(p_cur + j)}"]
 
-    # ---- row max of S(kt+1): block 0 (MFMAs 0..3) in slots 9..11, block 1 (4..7) in 13..15 ----
-    def nmax(m: int) -> list[str]:
-        plan = {9: (0, 6), 10: (6, 12), 11: (12, 16), 13: (16, 22), 14: (22, 28), 15: (28, 32)}
-        if m not in plan:
-            return []
-        lo, hi = plan[m]
-        if lo == 0:  # first: max3(s0, s1, s2), then pairs from 3 on
-            out = [f"v_max3_f32 {v(mx_nxt)}, {v(s_nxt)}, {v(s_nxt + 1)}, {v(s_nxt + 2)}"]
-            k = 3
-        else:
-            out, k = [], lo
-        while k + 1 < hi:
-            out.append(f"v_max3_f32 {v(mx_nxt)}, {v(mx_nxt)}, {v(s_nxt + k)}, {v(s_nxt + k + 1)}")
-            k += 2
-        if k < hi:
-            out.append(f"v_max_f32 {v(mx_nxt)}, {v(mx_nxt)}, {v(s_nxt + k)}")
-        return out
-
     # ---- copies ----
     # copy i of wave w fills LDS bytes (w + i*nw) * 1024 of the slot
     cpw = (TILE // 1024) // nw
@@ -220,24 +225,31 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
         L += expo(m)
         L += scale(m + 1) if m + 1 < 16 else ["s_nop 1"]
         L += pack(m)
-        if not kmask:
-            L += nmax(m)
         if m == 0:
             L += kcopy
         if m == 2:
             L += vcopy
-    L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
-    # ---- O rescale ----
-    L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{par}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
-    L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(32)]
-    L += [f"L_noscale_{par}_%=:"]
+    L += ["s_nop 2"]
+    if not kmask:
+        # ---- some P(kt) overflowed fp16 (its row sum is inf; or NaN): the row max of S(kt),
+        # the rescale of l and O, P(kt) and its row sum again ----
+        L += [f"v_cmp_ngt_f32 vcc, 0x7f800000, {v(LS)}", "s_nop 3", f"s_cbranch_vccz L_fits_{par}_%="]
+        L += row_max(s_cur) + rescale(f"{par}") + ["s_nop 7", "s_nop 7", "s_nop 7"] + o_scale()
+        L += [f"v_mov_b32 {v(LS)}, 0"] + scale(0)
+        for j in range(16):
+            L += expo(j) + (scale(j + 1) if j + 1 < 16 else ["s_nop 1"]) + pack(j)
+        L += ["s_nop 2", f"L_fits_{par}_%=:"]
+    L += [f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
+    if kmask:  # ---- O rescale ----
+        L += ["s_cmp_eq_u32 %[flag], 0", f"s_cbranch_scc1 L_noscale_{par}_%=", "s_nop 7", "s_nop 7", "s_nop 7"]
+        L += o_scale() + [f"L_noscale_{par}_%=:"]
     if kmask:
         L += [f"v_mov_b32 {v(ALPHA)}, {NEG_INF}",
               f"v_cndmask_b32 {v(MR)}, {v(MR)}, {v(ALPHA)}, s[{S_NOKEY}:{S_NOKEY + 1}]"]
     # ---- end: this step's copies have landed; barrier; next V slots ----
     L += ["s_waitcnt vmcnt(0) lgkmcnt(0)"]
     if kmask:  # the next tile's key bits
-        L += [f"v_cmp_ne_u32 vcc, 0, {v(mx_nxt)}", f"s_mov_b32 s{S_KB[0]}, vcc_lo",
+        L += [f"v_cmp_ne_u32 vcc, 0, {v(kb_nxt)}", f"s_mov_b32 s{S_KB[0]}, vcc_lo",
               f"s_mov_b32 s{S_KB[1]}, vcc_hi"]
     L += ["s_barrier",
           f"s_add_u32 %[vrd], %[vrd], {TILE}", f"s_cmp_eq_u32 %[vrd], {VSLOTS * TILE}",

@@ -96,13 +96,6 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
   constexpr int NM = NS + NP;  // MFMAs of the interleaved chunk region
   constexpr int NC = NM / 2 < 4 ? 4 : NM / 2;  // chunks per step
   constexpr int EPC = 32 / NC;             // score entries per lane per chunk
-  // chunk holding the last S^T MFMA, and the first chunk that reads its result
-  constexpr int C_LAST_S = [] {
-    int c = 0;
-    while (NS - 1 >= ((c + 1) * NM) / NC) ++c;
-    return c;
-  }();
-  constexpr int C_MAX = C_LAST_S + 2 < NC ? C_LAST_S + 2 : NC;
   static_assert(HD <= 64, "head_dim 128 takes the ring / pair / register bodies, 256 the generic kernel");
   static_assert(TILE % 1024 == 0, "tiles must be whole 1 KB copies");
   static_assert(32 % NC == 0 && EPC % 2 == 0, "chunks must split the 32 entries into pairs");
@@ -259,8 +252,12 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     int kbyte_next = 1;
     if (KMASK && HAS_NEXT) kbyte_next = key_byte(kt + 1);
 
-    float mx = mx_cur;
     const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
+    // Steps after the first on unmasked tiles (m_run finite) rescale only when needed: P(kt)
+    // is computed against m_run and, when some entry overflows fp16 (its row sum is then inf,
+    // or NaN), the tile's max moves m_run and P(kt) is computed again (after the slots below).
+    const bool fit_test = !KMASK && !need_mask && kt > 0;
+    float mx = mx_cur;
     if (need_mask) {
       // bit j of kbits: key k0 + 4*g + j is valid
       const uint64_t kbits = kbits_cur >> (4 * g);
@@ -276,19 +273,18 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
           mx = fmaxf(mx, s_cur[kb2][r]);
         }
     }
-    mx = pair_max(mx);
     const float cs = p.scale_log2;
+    // Lazy rescale (the other steps): the reference max m_run only moves when
+    // some row of the wave has grown by more than 2^8 over it, so exponentials
+    // stay <= 256 and the O/l rescale is skipped on most tiles; O and l always
+    // share one reference, so the final O/l is unchanged.  l (tiles < kt) is
+    // rescaled here.  With deferred P.V, O is rescaled at the end of the step,
+    // after the deferred MFMAs have added tile kt-1 at the old reference, so no
+    // MFMA writes O on a conditional path (an MFMA accumulator written on two
+    // paths is copied between register sets on every step).
+    mx = pair_max(mx);
     const float m_tile = mx * cs;  // cs > 0: max(s)*cs == max(s*cs)
-    // Lazy rescale: the reference max m_run only moves when some row of the
-    // wave has grown by more than 2^8 over it, so exponentials stay <= 256
-    // (exact in fp16's range) and the O/l rescale is skipped on most tiles;
-    // O and l always share one reference, so the final O/l is unchanged.
-    // l (tiles < kt) is rescaled here.  With deferred P.V, O is rescaled at
-    // the end of the step, after the deferred MFMAs have added tile kt-1 at
-    // the old reference, so no MFMA writes O on a conditional path (an MFMA
-    // accumulator written on two paths is copied between register sets on
-    // every step).
-    const bool rescale = __any(m_tile > m_run + 8.0f);
+    bool rescale = !fit_test && __any(m_tile > m_run + 8.0f);
     float alpha = 1.0f;
     if (rescale) {
       const float m_new = fmaxf(m_run, m_tile);
@@ -296,7 +292,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       m_run = m_new;
       l_run *= alpha;
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float m_use = m_run == -INFINITY ? 0.f : m_run;
 
     // ---- chunks: MFMAs m in [c*NM/NC, (c+1)*NM/NC): S^T(kt+1) first, then O^T(kt-1) ----
     const char* ks_n = kslot((kt + 1) % kKSlots);
@@ -332,7 +328,6 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
         ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
       }
     };
-    float mxn = -INFINITY;
     // Reads run three MFMAs ahead of their use.
     constexpr int RA = 3;
 #pragma unroll
@@ -356,19 +351,23 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       }
       if (c == C_K && kt + 2 < n_kt) copy_k(kt + 2);
       if (c == C_V && HAS_NEXT) copy_v(kt + 1);
-      // row max of S(kt+1), spread over the chunks after its last MFMA
-      if constexpr (C_MAX < NC) if (HAS_NEXT && c >= C_MAX) {
-        const int n = NC - C_MAX;
-        const int a = ((c - C_MAX) * 32) / n, z = ((c - C_MAX + 1) * 32) / n;
-#pragma unroll
-        for (int e = a; e < z; ++e) mxn = fmaxf(mxn, s_next[e >> 4][e & 15]);
-      }
     }
-    if (HAS_NEXT && C_MAX >= NC) {
+    if (fit_test && __any(!(ls < INFINITY))) {
+      float mxr = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 32; ++e) mxn = fmaxf(mxn, s_next[e >> 4][e & 15]);
+      for (int e = 0; e < 32; ++e) mxr = fmaxf(mxr, s_cur[e >> 4][e & 15]);
+      const float m_fit = pair_max(mxr) * cs;
+      const float m_new = fmaxf(m_run, m_fit);
+      alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      rescale = true;
+      m_use = m_run;
+      ls = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) exp_entry(e);
     }
-    mx_next = mxn;
+    mx_next = -INFINITY;  // the row max of a tile is taken in its own step
     l_run += ls;
     if (rescale) {
 #pragma unroll
@@ -436,7 +435,8 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
     if constexpr (HD == 64 && (NW == 4 || NW == 8) && CAUSAL) {
       if (groups > 0) {
         // Pinned: O^T v[64:95], Q v[96:111], the scores of tile kt v[112:143] (s_b), P of
-        // tile kt-1 v[144:159] (pf_a), their row max v160 (mx_b), m_run v161, l_run v162.
+        // tile kt-1 v[144:159] (pf_a), m_run v161, l_run v162; v160 (mx_b, no longer read
+        // after the loop) holds the key-masked loops' validity bytes.
         static_assert(HD == 64 && kKSlots == 2 && kVSlots == 3 && TILE == 8192 && CPW * NW == 8,
                       "the generated loop's layout");
         uint32_t ko[2] = {0, 0}, vo[2] = {0, 0};  // copies per wave: 2 at 4 waves, 1 at 8
@@ -465,7 +465,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
           [vb] "s"(vb), [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), \
           [cs] "s"(cs), [groups] "s"(groups)
 #define TK_STEPS64_CLOBS \
-          "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
+          "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
           "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", \
           "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", \
           "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", \
@@ -479,13 +479,13 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
 #include "tk_attn_steps64_kmask.inc"
                 : TK_STEPS64_OUTS, [koff] "+&v"(koff)
                 : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
-                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+                : TK_STEPS64_CLOBS, "v163", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
           } else {
             asm volatile(
 #include "tk_attn_steps64_w8_kmask.inc"
                 : TK_STEPS64_OUTS, [koff] "+&v"(koff)
                 : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
-                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+                : TK_STEPS64_CLOBS, "v163", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
           }
         } else if constexpr (NW == 4) {
           asm volatile(
