@@ -33,11 +33,10 @@ gen = _gen("gen_attn_epochs")
 gen64 = _gen("gen_attn_steps64")
 class _G64:
     """A head_dim-64 loop variant through the common generator interface."""
-    PINNED = gen64.PINNED
+    CLOBBERED, PINNED = gen64.CLOBBERED, gen64.PINNED
 
     def __init__(self, nw, kmask):
         self.nw, self.kmask = nw, kmask
-        self.CLOBBERED = gen64.KMASK_CLOBBERED if kmask else gen64.CLOBBERED
 
     def program(self):
         return gen64.program(self.nw, self.kmask)
@@ -418,14 +417,19 @@ def test_hd64_key_masked_loop_adds_only_the_mask_work(nw):
     in order; in place of the dense end-of-step overflow test it rescales at the start of
     the step (the lazy test on the row max of the masked scores, O scaled at the step end),
     and it adds the byte load, key bits, the selects and the m = -inf guard."""
+    # V fragment reads: the dense loop forms its two V bases once per step, the key-masked
+    # loop (whose v160/v163 hold validity bytes) one address per read
+    vaddr = lambda prog: [re.sub(r"^(ds_read_b64_tr_b16 v\[\d+:\d+\]), v\d+", r"\1, *", l) for l in prog]
     dense, _ = _hd64_refits(gen64.program(nw, False))
-    masked = gen64.program(nw, True)
+    dense = [l for l in vaddr(dense) if not l.startswith(("v_add_u32 v160, %[vrd]", "v_add_u32 v163, %[vrd]"))]
+    masked = vaddr(gen64.program(nw, True))
     check = (f"v_cmp_ngt_f32 vcc, 0x7f800000, v{gen64.LS}", "s_nop 3")
     kept = [l for l in dense if not l.startswith(("s_cbranch_vccz L_fits_", "L_fits_")) and l not in check]
     it = iter(masked)
     assert all(any(m == l for m in it) for l in kept)
     extra = [l for l in masked if l not in kept]
-    assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "s_waitcnt vmcnt", "v_cmp_", "s_mov_b32 s9",
+    assert all(l.startswith(("global_load_ubyte", "v_add_u32 %[koff]", "v_add_u32 v21", "s_waitcnt vmcnt", "v_cmp_",
+                             "s_mov_b32 s9",
                              "s_mov_b64 s[94:95]", "s_mov_b64 s[92:93], %[kbits]", "s_bfe_i32", "v_cndmask_b32", "v_mov_b32 v", "v_max",
                              "v_permlane32_swap", "v_mul_f32", "v_add_f32 v213", "v_sub_f32", "v_exp_f32 v216",
                              "s_nop", "s_cbranch_vccz L_norescale", "L_norescale", "s_mov_b32 %[flag]",

@@ -47,9 +47,11 @@ Register map (VGPRs; the asm statement pins or clobbers every one of them)
   v[96:111]   Q fragments, 4 x 4                            (in)
   v[112:143]  scores X: S(kt) at entry and exit             (in/out)
   v[144:159]  P tile W: P(kt-1) at entry and exit           (in/out)
-  v160        key-masked: validity bytes of the next tile   (in/out; unused without a mask)
+  v160        dense: V read base of head-dim block 0;       (in/out; dead after the loop)
+              key-masked: validity bytes of the next tile
   v161, v162  m_run, l_run                                  (in/out)
-  v163        key-masked: validity bytes (other parity)     (clobbered by the key-masked loops)
+  v163        dense: V read base of head-dim block 1;       (clobbered)
+              key-masked: validity bytes (other parity)
   v[164:195]  scores Y                                      (clobbered)
   v[196:211]  P tile Z                                      (clobbered)
   v212..v217  temporaries                                   (clobbered)
@@ -76,12 +78,12 @@ T0, T1, T2, T3 = 212, 213, 214, 215   # exponential pipeline, two pairs
 MX, TMP = T0, T1                      # the max phase ends before the pipeline starts
 ALPHA, LS = 216, 217
 RING = 218                            # 64-bit aligned tuples
+VA = (MXX, MXY)                       # dense loops: this step's V read bases (head-dim blocks 0, 1)
 TILE = 8192                           # bytes per K or V tile (64 rows x 128 bytes)
 KSLOTS, VSLOTS = 2, 3
 
 PINNED = set(range(64, 160)) | {MXX, MR, LR}
-CLOBBERED = list(range(164, 230))
-KMASK_CLOBBERED = sorted({MXY} | set(CLOBBERED))   # v163: the next tile's validity bytes
+CLOBBERED = sorted({MXY} | set(range(164, 230)))
 
 
 def v(a: int, n: int = 1) -> str:
@@ -141,7 +143,7 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
     k_rd = par * TILE                     # K(kt+1) is read from slot (kt + 1) % 2 = par
     k_wr = (1 - par) * TILE               # K(kt+2) is written into slot kt % 2
 
-    L = ["s_mov_b32 %[flag], 0"] if kmask else []
+    L = ["s_mov_b32 %[flag], 0"] if kmask else [f"v_add_u32 {v(VA[d])}, %[vrd], %[vl{d}]" for d in (0, 1)]
     L += [f"v_mov_b32 {v(LS)}, 0"]
     if kmask:
         L += [f"global_load_ubyte {v(kb_nxt)}, %[koff], %[kvb]", "v_add_u32 %[koff], 64, %[koff]"]
@@ -158,11 +160,12 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
         if m < 8:
             kb2, kk = m // 4, m % 4
             off = k_rd + kb2 * 4096
-            if kk == 0:
-                return [f"ds_read_b128 {v(r, 4)}, %[kl0] offset:{off}"]
-            return [f"v_xor_b32 {v(ka)}, {kk << 5}, %[kl0]", f"ds_read_b128 {v(r, 4)}, {v(ka)} offset:{off}"]
+            return [f"ds_read_b128 {v(r, 4)}, %[kl{kk}] offset:{off}"]  # kl{kk} = kl0 ^ (kk << 5)
         c = m - 8
         t, d = c // 2, c % 2
+        if not kmask:  # this step's V slot base, formed at the step start
+            return [f"ds_read_b64_tr_b16 {v(r, 2)}, {v(VA[d])} offset:{t * 2048}",
+                    f"ds_read_b64_tr_b16 {v(r + 2, 2)}, {v(VA[d])} offset:{t * 2048 + 1024}"]
         return [f"v_add_u32 {v(ka)}, %[vrd], %[vl{d}]",
                 f"ds_read_b64_tr_b16 {v(r, 2)}, {v(ka)} offset:{t * 2048}",
                 f"ds_read_b64_tr_b16 {v(r + 2, 2)}, {v(ka)} offset:{t * 2048 + 1024}"]

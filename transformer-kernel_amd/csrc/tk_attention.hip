@@ -436,7 +436,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       if (groups > 0) {
         // Pinned: O^T v[64:95], Q v[96:111], the scores of tile kt v[112:143] (s_b), P of
         // tile kt-1 v[144:159] (pf_a), m_run v161, l_run v162; v160 (mx_b, no longer read
-        // after the loop) holds the key-masked loops' validity bytes.
+        // after the loop) holds a V read base (dense) or validity bytes (key-masked).
         static_assert(HD == 64 && kKSlots == 2 && kVSlots == 3 && TILE == 8192 && CPW * NW == 8,
                       "the generated loop's layout");
         uint32_t ko[2] = {0, 0}, vo[2] = {0, 0};  // copies per wave: 2 at 4 waves, 1 at 8
@@ -461,11 +461,12 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
           [vwr] "+&s"(vwr), [msave] "=&s"(msave), [cnt] "=&s"(cnt), [flag] "=&s"(flag)
 #define TK_STEPS64_INS \
           [q0] "{v[96:99]}"(qf[0]), [q1] "{v[100:103]}"(qf[1]), [q2] "{v[104:107]}"(qf[2]), [q3] "{v[108:111]}"(qf[3]), \
-          [kl0] "v"(kl0), [vl0] "v"(vl0), [vl1] "v"(vl1), [kb] "s"(kb), \
+          [kl0] "v"(kl0), [kl1] "v"(kl0 ^ 32u), [kl2] "v"(kl0 ^ 64u), [kl3] "v"(kl0 ^ 96u), \
+          [vl0] "v"(vl0), [vl1] "v"(vl1), [kb] "s"(kb), \
           [vb] "s"(vb), [ldsw] "s"(ldsw), [kt2] "s"(kt2), [vt2] "s"(vt2), \
           [cs] "s"(cs), [groups] "s"(groups)
 #define TK_STEPS64_CLOBS \
-          "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
+          "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", \
           "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", \
           "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198", \
           "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", \
@@ -479,13 +480,13 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
 #include "tk_attn_steps64_kmask.inc"
                 : TK_STEPS64_OUTS, [koff] "+&v"(koff)
                 : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
-                : TK_STEPS64_CLOBS, "v163", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
           } else {
             asm volatile(
 #include "tk_attn_steps64_w8_kmask.inc"
                 : TK_STEPS64_OUTS, [koff] "+&v"(koff)
                 : TK_STEPS64_INS, [kvb] "s"(kvb), [kbits] "s"(kbits_cur)
-                : TK_STEPS64_CLOBS, "v163", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
+                : TK_STEPS64_CLOBS, "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95");
           }
         } else if constexpr (NW == 4) {
           asm volatile(
