@@ -345,8 +345,10 @@ def test_hd64_loop_covers_two_steps_of_16_mfmas():
     # 32 exponentials and 16 packs per step, every row-sum term in order
     temps = tuple(f"v_exp_f32 v{r}," for r in (gen64.T0, gen64.T1, gen64.T2, gen64.T3))
     assert sum(1 for l in main if l.startswith(temps)) == 2 * 32
-    dots = [l for l in main if l.startswith("v_dot2c")]
-    assert len(dots) == 32
+    sums = [l for l in main if l.startswith(f"v_add_f32 v{gen64.LS}, v{gen64.LS}, ")]
+    assert len(sums) == 64  # the fp32 exponentials, one add each, in entry order
+    exps = [l.split()[1].rstrip(",") for l in main if l.startswith(temps)]
+    assert [l.split()[-1] for l in sums] == exps
     # no row max on the main path: the rescale runs only when a P entry overflows fp16
     assert not any(l.startswith(("v_max", "v_permlane")) for l in main)
 
@@ -359,7 +361,7 @@ def test_hd64_refit_recomputes_p_as_the_step_does():
     prog = gen64.program()
     main, refits = _hd64_refits(prog)
     assert len(refits) == 2
-    p_ops = ("v_fma_f32", "v_exp_f32", "v_cvt_pk_f16_f32", "v_dot2c_f32_f16")
+    p_ops = ("v_fma_f32", "v_exp_f32", "v_cvt_pk_f16_f32", f"v_add_f32 v{gen64.LS}, v{gen64.LS}")
     steps = [[], []]
     k = 0
     for l in main:
@@ -378,8 +380,8 @@ def test_hd64_refit_recomputes_p_as_the_step_does():
         assert r.index(f"v_mov_b32 v{gen64.MR}, v{gen64.TMP}") < reset
         o_muls = [l for l in r if l.startswith("v_mul_f32 v") and int(l.split()[1][1:-1]) in range(64, 96)]
         assert len(o_muls) == 32
-    # the overflow test reads the finished row sum: inf or NaN take the refit
-    assert sum(1 for l in main if l == f"v_cmp_ngt_f32 vcc, 0x7f800000, v{gen64.LS}") == 2
+    # the overflow test reads the finished row sum: >= 65504 (the fp16 maximum) or NaN refit
+    assert sum(1 for l in main if l == f"v_cmp_ngt_f32 vcc, 0x477fe000, v{gen64.LS}") == 2
 
 
 def test_hd64_loops_differ_only_in_the_copies():
@@ -423,7 +425,7 @@ def test_hd64_key_masked_loop_adds_only_the_mask_work(nw):
     dense, _ = _hd64_refits(gen64.program(nw, False))
     dense = [l for l in vaddr(dense) if not l.startswith(("v_add_u32 v160, %[vrd]", "v_add_u32 v163, %[vrd]"))]
     masked = vaddr(gen64.program(nw, True))
-    check = (f"v_cmp_ngt_f32 vcc, 0x7f800000, v{gen64.LS}", "s_nop 3")
+    check = (f"v_cmp_ngt_f32 vcc, 0x477fe000, v{gen64.LS}", "s_nop 3")
     kept = [l for l in dense if not l.startswith(("s_cbranch_vccz L_fits_", "L_fits_")) and l not in check]
     it = iter(masked)
     assert all(any(m == l for m in it) for l in kept)

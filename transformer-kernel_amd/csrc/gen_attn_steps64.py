@@ -13,10 +13,11 @@ Step kt of the DMA body (key tile kt = keys 64kt .. 64kt+63), for every wave:
   16 slots  slot m < 8: S^T(kt+1) MFMA m (key block m / 4, k-step m % 4);
             slot m >= 8: O^T += V^T(kt-1) . P^T(kt-1), MFMA m - 8 (head-dim block (m-8) % 2,
             P block (m-8) / 2); exponential pair m of S(kt) (entries 2m, 2m+1) between the
-            MFMAs -> P(kt) = exp2(cs*S(kt) - m_run), fp16 row sum with v_dot2c
+            MFMAs -> P(kt) = exp2(cs*S(kt) - m_run) in fp16, row sum of the fp32 exponentials
   copies    K tile kt+2 after slot 0, V tile kt+1 after slot 2 (LDS DMA)
-  fit       the reference m_run moves only when some P(kt) entry overflows fp16 (>= 2^16: the
-            row sum is then inf; a NaN score also lands here): then m_tile = cs * (row max of
+  fit       the reference m_run moves only when the row sum reaches 65504, the fp16 maximum
+            (so before any P(kt) entry could overflow fp16; a NaN also lands here): then
+            m_tile = cs * (row max of
             S(kt) over the lane pair), m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new),
             l_run *= alpha, O *= alpha (O holds tiles < kt), and P(kt) and its row sum again
   end       l_run += row sum; wait for this step's copies; barrier
@@ -59,7 +60,7 @@ Register map (VGPRs; the asm statement pins or clobbers every one of them)
 
 Wait states: as in gen_attn_epochs.py (M0 -> LDS DMA 1, MFMA -> VALU 24 or an MFMA-free
 stretch of at least 18 instructions, VALU -> v_permlane32_swap 2, VCC -> s_cbranch_vccz 4,
-v_exp -> VALU 1, v_dot2c -> other VALU 3).
+v_exp -> VALU 1).
 """
 from __future__ import annotations
 
@@ -78,6 +79,7 @@ T0, T1, T2, T3 = 212, 213, 214, 215   # exponential pipeline, two pairs
 MX, TMP = T0, T1                      # the max phase ends before the pipeline starts
 ALPHA, LS = 216, 217
 RING = 218                            # 64-bit aligned tuples
+FP16_MAX = "0x477fe000"                # 65504.0
 VA = (MXX, MXY)                       # dense loops: this step's V read bases (head-dim blocks 0, 1)
 TILE = 8192                           # bytes per K or V tile (64 rows x 128 bytes)
 KSLOTS, VSLOTS = 2, 3
@@ -190,8 +192,9 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
 
     def pack(j: int) -> list[str]:
         a, b = tp[j % 2]
-        return [f"v_cvt_pk_f16_f32 {v(p_cur + j)}, {v(a)}, {v(b)}",
-                f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(p_cur + j)}"]
+        return [f"v_cvt_pk_f16_f32 {v(p_cur + j)}, {v(a)}, {v(b)}",   # P(kt) pair j in fp16
+                f"v_add_f32 {v(LS)}, {v(LS)}, {v(a)}",                   # row sum of the fp32
+                f"v_add_f32 {v(LS)}, {v(LS)}, {v(b)}"]                   # exponentials, in order
 
     # ---- copies ----
     # copy i of wave w fills LDS bytes (w + i*nw) * 1024 of the slot
@@ -234,9 +237,9 @@ def step(par: int, nw: int = 4, kmask: bool = False) -> list[str]:
             L += vcopy
     L += ["s_nop 2"]
     if not kmask:
-        # ---- some P(kt) overflowed fp16 (its row sum is inf; or NaN): the row max of S(kt),
-        # the rescale of l and O, P(kt) and its row sum again ----
-        L += [f"v_cmp_ngt_f32 vcc, 0x7f800000, {v(LS)}", "s_nop 3", f"s_cbranch_vccz L_fits_{par}_%="]
+        # ---- the row sum reached the fp16 maximum (an entry of P(kt) may have overflowed; or
+        # NaN): the row max of S(kt), the rescale of l and O, P(kt) and its row sum again ----
+        L += [f"v_cmp_ngt_f32 vcc, {FP16_MAX}, {v(LS)}", "s_nop 3", f"s_cbranch_vccz L_fits_{par}_%="]
         L += row_max(s_cur) + rescale(f"{par}") + ["s_nop 7", "s_nop 7", "s_nop 7"] + o_scale()
         L += [f"v_mov_b32 {v(LS)}, 0"] + scale(0)
         for j in range(16):

@@ -254,8 +254,9 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
 
     const bool need_mask = (k0 + kBN > p.S) || (CAUSAL && k0 + kBN - 1 > wave_row_min) || KMASK;
     // Steps after the first on unmasked tiles (m_run finite) rescale only when needed: P(kt)
-    // is computed against m_run and, when some entry overflows fp16 (its row sum is then inf,
-    // or NaN), the tile's max moves m_run and P(kt) is computed again (after the slots below).
+    // is computed against m_run and, when its row sum reaches 65504 (the fp16 maximum, so
+    // before any entry could overflow fp16; or NaN), the tile's max moves m_run and P(kt) is
+    // computed again (after the slots below).
     const bool fit_test = !KMASK && !need_mask && kt > 0;
     float mx = mx_cur;
     if (need_mask) {
@@ -325,7 +326,16 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
         const f16x2 hp = {(f16)pe[e - 1], (f16)pe[e]};
         p_cur[e >> 3][(e & 7) - 1] = hp[0];
         p_cur[e >> 3][e & 7] = hp[1];
-        ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+        // Row sum.  Causal: the fp32 exponentials in entry order, as the asm loop (two
+        // adds per pair cost less beside the MFMAs than one fp16 dot of the packed pair);
+        // non-causal (no asm loop): the fp16 dot, which keeps these instantiations within
+        // 256 VGPRs without scratch.
+        if constexpr (CAUSAL) {
+          ls += pe[e - 1];
+          ls += pe[e];
+        } else {
+          ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+        }
       }
     };
     // Reads run three MFMAs ahead of their use.
@@ -352,7 +362,7 @@ __device__ __forceinline__ void flash_dma_body(const AttnArgs& p) {
       if (c == C_K && kt + 2 < n_kt) copy_k(kt + 2);
       if (c == C_V && HAS_NEXT) copy_v(kt + 1);
     }
-    if (fit_test && __any(!(ls < INFINITY))) {
+    if (fit_test && __any(!(ls < 65504.0f))) {
       float mxr = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 32; ++e) mxr = fmaxf(mxr, s_cur[e >> 4][e & 15]);
@@ -1585,8 +1595,9 @@ __device__ __forceinline__ void flash_pair_body(const AttnArgs& p) {
 // next-tile scores, no deferred P, no copy ring -- so it needs about a third
 // of flash_dma_body's registers and 16 KB of LDS, and all workgroups of such
 // a launch are resident at once.  For one tile the DMA body's running max is
-// the tile max, so the operand layouts, the exponentials, the fp16 row sums
-// and the MFMA order here are the same and the results are identical.
+// the tile max, so the operand layouts, the exponentials, the row sums (of the
+// fp32 exponentials, as the causal DMA body) and the MFMA order here are the
+// same and the results are identical.
 template <int HD, int NW, bool CAUSAL, bool KMASK>
 __device__ __forceinline__ void flash_single_body(const AttnArgs& p) {
   constexpr int BM = 32 * NW;

@@ -89,11 +89,13 @@ __device__ __forceinline__ void attend_one_tile(const char* ks_, const char* vs_
   float ls = 0.f;
 #pragma unroll
   for (int e = 0; e < 32; e += 2) {
-    const f16x2 hp = {(f16)__builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use)),
-                      (f16)__builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use))};
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], cs, -m_use));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[(e + 1) >> 4][(e + 1) & 15], cs, -m_use));
+    const f16x2 hp = {(f16)p0, (f16)p1};
     pf[e >> 3][e & 7] = hp[0];
     pf[e >> 3][(e & 7) + 1] = hp[1];
-    ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(hf16x2, hp), ones, ls, false);
+    ls += p0;  // row sum of the fp32 exponentials, in entry order (as flash_dma_body)
+    ls += p1;
   }
 
   // ---- O^T = V^T . P^T; V^T operands by transposed LDS reads ----
