@@ -81,6 +81,15 @@ __device__ __forceinline__ void tile_of_block(int id, int tiles_m, int tiles_n, 
   tn = in_group / gsize;
 }
 
+// threadIdx.x through an empty asm: in the persistent kernel's tile loop the
+// per-lane addresses derived from it are then formed per tile instead of
+// being hoisted out of the loop and kept live across it (they spilled).
+__device__ __forceinline__ int laundered_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
 __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
@@ -218,42 +227,68 @@ struct Mainloop {
   // after its last compute phase, so both groups pass 2 * nk barriers.  Per
   // accumulator the k order is run_direct's, so the results are bit-identical
   // to it.
-  __device__ __forceinline__ static void run_pingpong(const GemmArgs& p, int m0, int n0, f16* smem,
-                                                      f32x16 (&acc)[FN][FM]) {
-    static_assert(BM == 256 && BN == 256 && WAVES_M == 4 && WAVES_N == 2 && BK == 64 && STAGES == 2 &&
-                      DIRECT && WG == 0 && A_INSTS == 4 && W_INSTS == 4,
-                  "ping-pong: 256 x 256 tile, 4 x 2 waves, BK 64, two stages");
-    constexpr int STAGE_BYTES = BM * BK * 2;  // one operand's K-tile: 32 KB
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave % WAVES_M;
-    const int grp = wave / WAVES_M;  // = wn
-    const uint32_t lds_a = (uint32_t)(size_t)(lds_char*)smem + wave * A_INSTS * 1024;
-    const uint32_t lds_w = lds_a + STAGES * STAGE_BYTES;
-    const int nk = p.K / BK;  // even and at least 2 (the dispatch checks K > 0, K % 128 == 0)
-    // Copy c of a wave covers 8 rows (lane / 8 within them) of A (c < 4) or W;
-    // the lane fetches the logical chunk that the LDS swizzle stores at
-    // physical chunk lane % 8 of its row, (lane % 8) ^ ((row >> 1) & 7), which
-    // for these rows is (lane % 8) ^ (4 * (c & 1) + lane / 16).
-    uint32_t vo_a[2], vo_w[2];
+  // The ping-pong loop's copy addressing for output tile (m0, n0): wave w's
+  // copies of a K-tile.  Copy c of a wave covers 8 rows (lane / 8 within
+  // them) of A (c < 4) or W; the lane fetches the logical chunk that the LDS
+  // swizzle stores at physical chunk lane % 8 of its row,
+  // (lane % 8) ^ ((row >> 1) & 7), which for these rows is
+  // (lane % 8) ^ (4 * (c & 1) + lane / 16).
+  struct PPCopies {
+    static constexpr int STAGE_BYTES = BM * BK * 2;  // one operand's K-tile: 32 KB
+    uint32_t lds_a, lds_w, vo_a[2], vo_w[2], row8_a, row8_w;
+    i32x4 rs_a, rs_w;
+    __device__ __forceinline__ PPCopies(const GemmArgs& p, int m0, int n0, f16* smem, int lane, int wave) {
+      lds_a = (uint32_t)(size_t)(lds_char*)smem + wave * A_INSTS * 1024;
+      lds_w = lds_a + STAGES * STAGE_BYTES;
 #pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const uint32_t ch = (uint32_t)((lane & 7) ^ (4 * par + (lane >> 4)));
-      vo_a[par] = (uint32_t)((lane >> 3) * p.lda * 2) + (ch << 4);
-      vo_w[par] = (uint32_t)((lane >> 3) * p.ldw * 2) + (ch << 4);
+      for (int par = 0; par < 2; ++par) {
+        const uint32_t ch = (uint32_t)((lane & 7) ^ (4 * par + (lane >> 4)));
+        vo_a[par] = (uint32_t)((lane >> 3) * p.lda * 2) + (ch << 4);
+        vo_w[par] = (uint32_t)((lane >> 3) * p.ldw * 2) + (ch << 4);
+      }
+      // buffer bases: this wave's first copy row; byte offsets per copy and K-tile
+      rs_a = raw_buffer_rsrc(p.a + (int64_t)(m0 + wave * A_INSTS * 8) * p.lda);
+      rs_w = raw_buffer_rsrc(p.w + (int64_t)(n0 + wave * W_INSTS * 8) * p.ldw);
+      row8_a = (uint32_t)(16 * p.lda);  // 8 rows, bytes
+      row8_w = (uint32_t)(16 * p.ldw);
     }
-    // buffer bases: this wave's first copy row; byte offsets per copy and K-tile
-    const i32x4 rs_a = raw_buffer_rsrc(p.a + (int64_t)(m0 + wave * A_INSTS * 8) * p.lda);
-    const i32x4 rs_w = raw_buffer_rsrc(p.w + (int64_t)(n0 + wave * W_INSTS * 8) * p.ldw);
-    const uint32_t row8_a = (uint32_t)(16 * p.lda), row8_w = (uint32_t)(16 * p.ldw);  // 8 rows, bytes
-    auto copies = [&](int kt, int stage) {
+    __device__ __forceinline__ void operator()(int kt, int stage) const {
 #pragma unroll
       for (int c = 0; c < A_INSTS; ++c)
         dma16_buf(rs_a, c * row8_a + kt * (BK * 2), vo_a[c & 1], lds_a + stage * STAGE_BYTES + c * 1024);
 #pragma unroll
       for (int c = 0; c < W_INSTS; ++c)
         dma16_buf(rs_w, c * row8_w + kt * (BK * 2), vo_w[c & 1], lds_w + stage * STAGE_BYTES + c * 1024);
-    };
+    }
+  };
+
+  // K-tile 0 of output tile (m0, n0) into stage 0, this wave's share (INSTS
+  // copies): issued by the persistent kernel before the previous tile's
+  // output stores, so the next run_pingpong starts with it in flight.
+  __device__ __forceinline__ static void pp_prefetch(const GemmArgs& p, int m0, int n0, f16* smem) {
+    const int tid = laundered_tid();
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    PPCopies(p, m0, n0, smem, lane, wave)(0, 0);
+  }
+
+  // PF >= 0: K-tile 0 was prefetched into stage 0 (pp_prefetch) when
+  // `prefetched`, and exactly PF vector-memory instructions of this wave were
+  // issued after it (the previous tile's stores), which may stay in flight.
+  template <int PF = -1>
+  __device__ __forceinline__ static void run_pingpong(const GemmArgs& p, int m0, int n0, f16* smem,
+                                                      f32x16 (&acc)[FN][FM], bool prefetched = false) {
+    static_assert(BM == 256 && BN == 256 && WAVES_M == 4 && WAVES_N == 2 && BK == 64 && STAGES == 2 &&
+                      DIRECT && WG == 0 && A_INSTS == 4 && W_INSTS == 4,
+                  "ping-pong: 256 x 256 tile, 4 x 2 waves, BK 64, two stages");
+    static_assert(PF < 0 || PF + INSTS < 64, "vmcnt range");
+    const int tid = PF >= 0 ? laundered_tid() : (int)threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WAVES_M;
+    const int grp = wave / WAVES_M;  // = wn
+    const int nk = p.K / BK;  // even and at least 2 (the dispatch checks K > 0, K % 128 == 0)
+    const PPCopies copies(p, m0, n0, smem, lane, wave);
     // Fragment reads: lane byte offsets of k-step kk in the wave's first A and
     // W row block of stage 0; the swizzle term depends on the row only
     // through frow (block rows are multiples of 32), so the other blocks and
@@ -319,12 +354,24 @@ struct Mainloop {
 
     // tile 0 (every wave its share) and group 1's share of tile 1; then
     // group 1 falls one phase behind
-    copies(0, 0);
-    if (grp == 1) {
-      copies(1, 1);
-      wait_vmcnt<INSTS>();
+    if constexpr (PF >= 0) {
+      if (!prefetched) copies(0, 0);
+      if (grp == 1) {
+        copies(1, 1);
+        if (prefetched) wait_vmcnt<PF + INSTS>();  // the prefetched tile 0 has landed
+        else wait_vmcnt<INSTS>();
+      } else {
+        if (prefetched) wait_vmcnt<PF>();
+        else wait_vmcnt<0>();
+      }
     } else {
-      wait_vmcnt<0>();
+      copies(0, 0);
+      if (grp == 1) {
+        copies(1, 1);
+        wait_vmcnt<INSTS>();
+      } else {
+        wait_vmcnt<0>();
+      }
     }
     phase_barrier();
     if (grp == 1) phase_barrier();
@@ -659,6 +706,74 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
 }
 
 
+// The fp16 epilogue (bias, bias + GELU) of the persistent ping-pong kernel,
+// whole 256 x 256 tiles: the passes of store_tile_lds one 32-row block at a
+// time (8 KB per wave) in the stage-1 half of the main-loop LDS (waves 0-3 in
+// A's stage 1, 4-7 in W's), so that stage 0 can take the next tile's first
+// K-tile (pp_prefetch, when has_next).  The bias vectors are loaded once,
+// before the first pass: a load issued after a store or after the prefetch
+// would make the compiler's wait for it also wait for those (the vector
+// memory counter retires in order).  The prefetch goes out after the last
+// pass is staged and before that pass's kPfStores output stores.
+constexpr int kPfStores = 8;
+template <class ML, int WAVES_M, int EPI>
+__device__ __forceinline__ void store_tile_lds_pf(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
+                                                  int n0, f16* smem, bool has_next, int next_m0, int next_n0) {
+  constexpr int WM = ML::WM, WN = ML::WN, FM = ML::FM, FN = ML::FN;
+  constexpr int ROWB = WN * 2;
+  constexpr int CPR = ROWB / 16;
+  constexpr int EPC = 8;  // elements per chunk
+  constexpr int TOT = 32 * CPR;
+  static_assert(ML::PINGPONG && WAVES_M == 4 && ROWB == 256 && TOT % 64 == 0, "256 x 256 ping-pong tile");
+  static_assert(TOT / 64 == kPfStores, "store count after the prefetch");
+  const int tid = laundered_tid();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int mw = m0 + (wave % WAVES_M) * WM;
+  const int nw = n0 + (wave / WAVES_M) * WN;
+  // stage 1: A at 32 KB, W at 96 KB; 8 KB (32 rows x 256 bytes) per wave
+  char* region = reinterpret_cast<char*>(smem) + (wave < 4 ? 32768 + wave * 8192 : 98304 + (wave - 4) * 8192);
+  f32x4 bias[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      bias[i][q] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw + i * 32 + 8 * q + 4 * (lane >> 5))
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jb = 0; jb < FM; ++jb) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = i * 32 + 8 * q + 4 * (lane >> 5);  // 4 consecutive n of this lane
+        const f32x4 b4 = bias[i][q];
+        const int row = lane & 31;
+        const f32x16& a = acc[i][jb];
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = a[4 * q + e] + b4[e];
+          if constexpr (EPI == TK_EPI_BIAS_GELU) v[e] = gelu_erf(v[e]);
+        }
+        *reinterpret_cast<f16x4*>(region + epi_off<CPR>(row, nl / 8) + (nl % 8) * 2) =
+            f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+      }
+    }
+    asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
+    if (jb == FM - 1 && has_next) ML::pp_prefetch(p, next_m0, next_n0, smem);
+#pragma unroll
+    for (int idx0 = 0; idx0 < TOT; idx0 += 64) {
+      const int idx = idx0 + lane;
+      const int row = idx / CPR, ch = idx % CPR;
+      const int m = mw + jb * 32 + row;
+      const int n = nw + ch * EPC;
+      const f16x8 d = *reinterpret_cast<const f16x8*>(region + epi_off<CPR>(row, ch));
+      *reinterpret_cast<f16x8*>(reinterpret_cast<f16*>(p.c) + (int64_t)m * p.ldc + n) = d;
+    }
+    asm volatile("" ::: "memory");
+  }
+}
+
 // One pass of the fp32 residual epilogue over accumulator blocks
 // [JB, JB + JC) of a wave:  C[m, n] = resid[m, n] + (acc + bias[n])  (C may
 // alias resid: every element is read and written by the same lane).  The
@@ -801,6 +916,38 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
     store_tile_resid<ML, T::WAVES_M, EPI == kEpiResidRows, ML::PINGPONG>(p, acc, tm * BM, tn * BN, smem);
   else
     store_tile_lds<ML, T::WAVES_M, EPI, ML::PINGPONG>(p, acc, tm * BM, tn * BN, smem);
+}
+
+// Persistent ping-pong GEMM (whole 256 x 256 tiles, fp16 epilogues): block b
+// runs tiles b, b + gridDim.x, ... (one XCD each, as tile_of_block expects).
+// Before a tile's output stores it copies the next tile's first K-tile into
+// stage 0, so the next K loop neither waits for that copy's latency nor for
+// the stores to drain (its first waits leave them in flight).  Between tiles
+// one barrier after an LDS-only wait: every wave's staging reads of stage 1
+// are done before group 1 refills it; the output stores stay in flight.
+template <class T, int EPI>
+__global__ __launch_bounds__(T::NT) void gemm_pf_kernel(GemmArgs p) {
+  constexpr int BM = T::BM, BN = T::BN;
+  using ML = typename T::template ML<true>;
+  static_assert(ML::PINGPONG && (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU), "fp16 epilogues, ping-pong loop");
+  __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
+  const int tiles_m = p.M / BM, tiles_n = p.N / BN;
+  const int tiles = tiles_m * tiles_n;
+  bool prefetched = false;
+  for (int id = blockIdx.x; id < tiles; id += gridDim.x) {
+    int tm, tn;
+    tile_of_block(id, tiles_m, tiles_n, tm, tn);
+    const int next = id + (int)gridDim.x;
+    int ntm = 0, ntn = 0;
+    if (next < tiles) tile_of_block(next, tiles_m, tiles_n, ntm, ntn);
+    f32x16 acc[ML::FN][ML::FM];
+    ML::zero(acc);
+    ML::template run_pingpong<kPfStores>(p, tm * BM, tn * BN, smem, acc, prefetched);
+    store_tile_lds_pf<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem, next < tiles, ntm * BM, ntn * BN);
+    wait_lgkm0();
+    phase_barrier();
+    prefetched = next < tiles;
+  }
 }
 
 // Full-row variant: BN == N, so each block owns complete output rows and
@@ -946,6 +1093,12 @@ using TileBigPP = Tile<256, 256, 4, 2, 64, 2, true>;  // the same, ping-pong K l
 using TileMid = Tile<128, 128, 2, 2, 64, 2>;   // 4 waves of 64 x 64, 2 blocks per CU
 using TileSmall = Tile<64, 64, 1, 1, 64, 2>;   // 1 wave
 
+#ifndef TK_GEMM_PF
+#define TK_GEMM_PF 1
+#endif
+constexpr bool kGemmPf = TK_GEMM_PF;
+constexpr int kPfGrid = 256;  // one persistent workgroup per CU
+
 template <int EPI>
 int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
@@ -959,8 +1112,15 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   // unchanged.
   // (its epilogues also assume vector-aligned output rows and bias).
   if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0 && p.vec &&
-      (p.bias == nullptr || p.bias16))
+      (p.bias == nullptr || p.bias16)) {
+    if constexpr (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU) {
+      if (kGemmPf && p.kvec && t256 >= 2 * kPfGrid) {
+        hipLaunchKernelGGL((gemm_pf_kernel<TileBigPP, EPI>), dim3((unsigned)kPfGrid), dim3(TileBigPP::NT), 0, st, p);
+        return check_launch("tk_gemm");
+      }
+    }
     return launch_gemm<TileBigPP, EPI>(p, st);
+  }
   // Other shapes, with the two-stage loop: 256x256 tiles win when they fill
   // whole rounds of the 256 CUs (or at least two rounds); with a partial last
   // round (e.g. 384 tiles) the 128x128 tile, two blocks per CU, is 5-10 %
