@@ -1114,7 +1114,7 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0 && p.vec &&
       (p.bias == nullptr || p.bias16)) {
     if constexpr (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU) {
-      if (kGemmPf && p.kvec && t256 >= 2 * kPfGrid) {
+      if (kGemmPf && p.kvec && t256 > kPfGrid) {  // some workgroup runs two or more tiles
         hipLaunchKernelGGL((gemm_pf_kernel<TileBigPP, EPI>), dim3((unsigned)kPfGrid), dim3(TileBigPP::NT), 0, st, p);
         return check_launch("tk_gemm");
       }
