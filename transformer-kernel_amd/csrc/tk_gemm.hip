@@ -710,12 +710,12 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const f32x16 (
 // whole 256 x 256 tiles: the passes of store_tile_lds one 32-row block at a
 // time (8 KB per wave) in the stage-1 half of the main-loop LDS (waves 0-3 in
 // A's stage 1, 4-7 in W's), so that stage 0 can take the next tile's first
-// K-tile (pp_prefetch, when has_next).  The bias vectors are loaded once,
-// before the first pass: a load issued after a store or after the prefetch
-// would make the compiler's wait for it also wait for those (the vector
-// memory counter retires in order).  The prefetch goes out after the last
-// pass is staged and before that pass's kPfStores output stores.
-constexpr int kPfStores = 8;
+// K-tile (pp_prefetch, when has_next).  The bias vectors are loaded, and
+// waited for, first: a load issued after a store or after the prefetch would
+// make the compiler's wait for it also wait for those (the vector memory
+// counter retires in order).  Then the prefetch, then the passes with their
+// kPfStores output stores, all of which may stay in flight into the next tile.
+constexpr int kPfStores = 16;
 template <class ML, int WAVES_M, int EPI>
 __device__ __forceinline__ void store_tile_lds_pf(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
                                                   int n0, f16* smem, bool has_next, int next_m0, int next_n0) {
@@ -725,7 +725,7 @@ __device__ __forceinline__ void store_tile_lds_pf(const GemmArgs& p, const f32x1
   constexpr int EPC = 8;  // elements per chunk
   constexpr int TOT = 32 * CPR;
   static_assert(ML::PINGPONG && WAVES_M == 4 && ROWB == 256 && TOT % 64 == 0, "256 x 256 ping-pong tile");
-  static_assert(TOT / 64 == kPfStores, "store count after the prefetch");
+  static_assert(FM * (TOT / 64) == kPfStores, "store count after the prefetch");
   const int tid = laundered_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int mw = m0 + (wave % WAVES_M) * WM;
@@ -739,6 +739,11 @@ __device__ __forceinline__ void store_tile_lds_pf(const GemmArgs& p, const f32x1
     for (int q = 0; q < 4; ++q)
       bias[i][q] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw + i * 32 + 8 * q + 4 * (lane >> 5))
                           : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) asm volatile("" ::"v"(bias[i][q]));  // the loads have returned here
+  if (has_next) ML::pp_prefetch(p, next_m0, next_n0, smem);
 #pragma unroll
   for (int jb = 0; jb < FM; ++jb) {
 #pragma unroll
@@ -760,7 +765,6 @@ __device__ __forceinline__ void store_tile_lds_pf(const GemmArgs& p, const f32x1
       }
     }
     asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
-    if (jb == FM - 1 && has_next) ML::pp_prefetch(p, next_m0, next_n0, smem);
 #pragma unroll
     for (int idx0 = 0; idx0 < TOT; idx0 += 64) {
       const int idx = idx0 + lane;
