@@ -157,8 +157,8 @@ GEMM_SHAPES = [  # one or more per tile configuration of the dispatch, direct an
     (1024, 1536, 512),    # C2 QKV (reduced M)
     (1024, 512, 2048),    # C2 FFN-down (reduced M)
     (4096, 4096, 1024),   # 256x256 tiles
-    (8192, 4352, 384),    # 544 256x256 tiles: the persistent ping-pong kernel (bias and GELU epilogues;
-                          # 2 or 3 tiles per workgroup, the next tile's first K-tile prefetched)
+    (8192, 4352, 384),    # 544 256x256 tiles: the persistent ping-pong kernel (bias, GELU and residual
+                          # epilogues; 2 or 3 tiles per workgroup, the next tile's first K-tile prefetched)
     (4096, 2048, 8192),   # C4 FFN-down (reduced M), long K: 128x128 tiles
     (1000, 200, 72),      # ragged M, N, K
     (77, 300, 8),         # tiny K

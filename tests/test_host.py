@@ -231,7 +231,7 @@ def test_hot_kernels_use_no_scratch():
     hot = [k for k in usage if any(s in k for s in ("gemm_kernel", "gemm_pf_kernel", "gemm_ln_kernel", "ln_rows_kernel",
                                                      "softmax_", "qkv_attn_kernel"))]
     assert len(hot) >= 30
-    assert sum(1 for k in hot if "gemm_pf_kernel" in k) == 2  # persistent ping-pong: bias, bias + GELU
+    assert sum(1 for k in hot if "gemm_pf_kernel" in k) == 3  # persistent ping-pong: bias, GELU, residual
     for name, hd, nw, causal in BENCH_ATTENTION:
         hot.append(f"_ZN2tk12_GLOBAL__N_1{len(name)}{name}ILi{hd}ELi{nw}ELb{causal}ELb0EEEvNS0_8AttnArgsE")
     # every head_dim-128 instantiation, the padding-mask (key-validity) ones included:

@@ -84,7 +84,6 @@ __device__ __forceinline__ void attend_one_tile(const char* ks_, const char* vs_
   const float m_use = m_tile == -INFINITY ? 0.f : m_tile;
 
   // ---- P in fp16 (8 consecutive entries = one B operand) and its row sum ----
-  const auto ones = __builtin_bit_cast(hf16x2, 0x3c003c00u);
   f16x8 pf[4];
   float ls = 0.f;
 #pragma unroll

@@ -899,6 +899,90 @@ __device__ __forceinline__ void store_tile_resid(const GemmArgs& p, const f32x16
   if constexpr (JC < FM) resid_pass<ML, WAVES_M, JC, JC, ROWS, WHOLE>(p, acc, mw, nw, region);
 }
 
+// The fp32 residual epilogue (dense rows) of the persistent ping-pong kernel,
+// whole 256 x 256 tiles.  Four passes per wave, each over 32 rows x 64
+// columns (pass k: accumulator row block k / 2, column half k % 2), staged as
+// 8 KB per wave in the stage-1 half of the main-loop LDS (waves 0-3 in A's
+// stage 1, 4-7 in W's), so that stage 0 can take the next tile's first
+// K-tile.  Order of this wave's vector-memory instructions: bias loads
+// (waited for), the prefetch (when has_next), residual rows of pass 0, then
+// per pass k the residual rows of pass k + 1 before the output stores of
+// pass k.  A residual wait so never covers an output store issued before
+// it (the vector memory counter retires in order), the prefetch precedes
+// every residual load the compiler waits for, and the last kPfStores
+// instructions are the output stores of passes 2 and 3, which may stay in
+// flight into the next tile.  Per element the sum is resid + (acc + bias),
+// as in resid_pass, so the outputs are bit-identical to gemm_kernel's.
+template <class ML, int WAVES_M>
+__device__ __forceinline__ void store_tile_resid_pf(const GemmArgs& p, const f32x16 (&acc)[ML::FN][ML::FM], int m0,
+                                                    int n0, f16* smem, bool has_next, int next_m0, int next_n0) {
+  constexpr int FM = ML::FM, FN = ML::FN;
+  constexpr int CPR = 16;          // 16-byte chunks per staged row (64 fp32)
+  constexpr int RPI = 64 / CPR;    // rows per read-back step
+  constexpr int NIT = 32 / RPI;    // read-back steps (residual loads) per pass
+  constexpr int PASSES = FM * 2;
+  static_assert(ML::PINGPONG && WAVES_M == 4 && FM == 2 && FN == 4 && ML::WN == 128, "256 x 256 ping-pong tile");
+  static_assert(NIT * 2 == kPfStores, "output stores of the last two passes");
+  const int tid = laundered_tid();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int mw = m0 + (wave % WAVES_M) * ML::WM;
+  const int nw = n0 + (wave / WAVES_M) * ML::WN;
+  char* region = reinterpret_cast<char*>(smem) + (wave < 4 ? 32768 + wave * 8192 : 98304 + (wave - 4) * 8192);
+  const int ch = lane % CPR, row0 = lane / CPR;
+  f32x4 bias[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    bias[h] = p.bias ? *reinterpret_cast<const f32x4*>(p.bias + nw + h * 64 + ch * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) asm volatile("" ::"v"(bias[h]));  // the loads have returned here
+  if (has_next) ML::pp_prefetch(p, next_m0, next_n0, smem);
+  const uint32_t ldr = (uint32_t)p.ldr;
+  f32x4 r[2][NIT];
+  auto fetch = [&](int k, f32x4 (&rk)[NIT]) {
+    const float* rbase = p.resid + (int64_t)(mw + (k >> 1) * 32) * p.ldr + nw + (k & 1) * 64;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+      rk[it] = *reinterpret_cast<const f32x4*>(rbase + ((uint32_t)(it * RPI + row0) * ldr + ch * 4));
+  };
+  auto stage = [&](int k) {
+    const int jb = k >> 1, h = k & 1;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x16& a = acc[2 * h + ii][jb];
+        const int chunk = ii * 8 + 2 * q + (lane >> 5);  // 4 consecutive columns of this lane
+        *reinterpret_cast<f32x4*>(region + epi_off<CPR>(lane & 31, chunk)) =
+            f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+      }
+  };
+  auto combine = [&](int k, const f32x4 (&rk)[NIT]) {
+    const f32x4 b = bias[k & 1];
+    float* cbase = reinterpret_cast<float*>(p.c) + (int64_t)(mw + (k >> 1) * 32) * p.ldc + nw + (k & 1) * 64;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int row = it * RPI + row0;
+      const f32x4 d = *reinterpret_cast<const f32x4*>(region + epi_off<CPR>(row, ch));
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = rk[it][e] + (d[e] + b[e]);
+      *reinterpret_cast<f32x4*>(cbase + (int64_t)row * p.ldc + ch * 4) = o;
+    }
+  };
+  fetch(0, r[0]);
+  stage(0);
+  asm volatile("" ::: "memory");  // LDS accesses of one wave complete in order
+#pragma unroll
+  for (int k = 0; k < PASSES; ++k) {
+    if (k + 1 < PASSES) fetch(k + 1, r[(k + 1) & 1]);
+    asm volatile("" ::: "memory");  // the next pass's residual loads before this pass's stores
+    combine(k, r[k & 1]);
+    asm volatile("" ::: "memory");
+    if (k + 1 < PASSES) stage(k + 1);
+    asm volatile("" ::: "memory");
+  }
+}
+
 template <class T, int EPI, bool DIRECT>
 __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
   constexpr int BM = T::BM, BN = T::BN;
@@ -922,18 +1006,20 @@ __global__ __launch_bounds__(T::NT) void gemm_kernel(GemmArgs p) {
     store_tile_lds<ML, T::WAVES_M, EPI, ML::PINGPONG>(p, acc, tm * BM, tn * BN, smem);
 }
 
-// Persistent ping-pong GEMM (whole 256 x 256 tiles, fp16 epilogues): block b
-// runs tiles b, b + gridDim.x, ... (one XCD each, as tile_of_block expects).
-// Before a tile's output stores it copies the next tile's first K-tile into
-// stage 0, so the next K loop neither waits for that copy's latency nor for
-// the stores to drain (its first waits leave them in flight).  Between tiles
-// one barrier after an LDS-only wait: every wave's staging reads of stage 1
-// are done before group 1 refills it; the output stores stay in flight.
+// Persistent ping-pong GEMM (whole 256 x 256 tiles; fp16 epilogues and the
+// dense fp32 residual epilogue): block b runs tiles b, b + gridDim.x, ...
+// (one XCD each, as tile_of_block expects).  Before a tile's output stores it
+// copies the next tile's first K-tile into stage 0, so the next K loop
+// neither waits for that copy's latency nor for the stores to drain (its
+// first waits leave them in flight).  Between tiles one barrier after an
+// LDS-only wait: every wave's staging reads of stage 1 are done before group
+// 1 refills it; the output stores stay in flight.
 template <class T, int EPI>
 __global__ __launch_bounds__(T::NT) void gemm_pf_kernel(GemmArgs p) {
   constexpr int BM = T::BM, BN = T::BN;
   using ML = typename T::template ML<true>;
-  static_assert(ML::PINGPONG && (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU), "fp16 epilogues, ping-pong loop");
+  static_assert(ML::PINGPONG && (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU || EPI == TK_EPI_BIAS_RESID),
+                "bias, GELU or dense residual epilogue, ping-pong loop");
   __shared__ __attribute__((aligned(16))) f16 smem[ML::LDS_HALVES];
   const int tiles_m = p.M / BM, tiles_n = p.N / BN;
   const int tiles = tiles_m * tiles_n;
@@ -947,7 +1033,10 @@ __global__ __launch_bounds__(T::NT) void gemm_pf_kernel(GemmArgs p) {
     f32x16 acc[ML::FN][ML::FM];
     ML::zero(acc);
     ML::template run_pingpong<kPfStores>(p, tm * BM, tn * BN, smem, acc, prefetched);
-    store_tile_lds_pf<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem, next < tiles, ntm * BM, ntn * BN);
+    if constexpr (EPI == TK_EPI_BIAS_RESID)
+      store_tile_resid_pf<ML, T::WAVES_M>(p, acc, tm * BM, tn * BN, smem, next < tiles, ntm * BM, ntn * BN);
+    else
+      store_tile_lds_pf<ML, T::WAVES_M, EPI>(p, acc, tm * BM, tn * BN, smem, next < tiles, ntm * BM, ntn * BN);
     wait_lgkm0();
     phase_barrier();
     prefetched = next < tiles;
@@ -1117,7 +1206,7 @@ int gemm_dispatch(const GemmArgs& p, hipStream_t st) {
   // (its epilogues also assume vector-aligned output rows and bias).
   if (t256 >= 256 && p.M % 256 == 0 && p.N % 256 == 0 && p.K > 0 && p.K % 128 == 0 && p.vec &&
       (p.bias == nullptr || p.bias16)) {
-    if constexpr (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU) {
+    if constexpr (EPI == TK_EPI_BIAS || EPI == TK_EPI_BIAS_GELU || EPI == TK_EPI_BIAS_RESID) {
       if (kGemmPf && p.kvec && t256 > kPfGrid) {  // some workgroup runs two or more tiles
         hipLaunchKernelGGL((gemm_pf_kernel<TileBigPP, EPI>), dim3((unsigned)kPfGrid), dim3(TileBigPP::NT), 0, st, p);
         return check_launch("tk_gemm");
