@@ -222,8 +222,8 @@ def test_generated_loop_meets_the_wait_states(loop):
 @pytest.mark.parametrize("planted", ["dot2c", "exp", "mfma", "m0", "permlane"])
 def test_wait_state_checker_finds_planted_mistakes(planted):
     prog = _asm_lines(gen.program())
-    if planted == "dot2c":  # the l_run update right after the last row-sum dot
-        i = next(i for i, l in enumerate(prog) if l.startswith("v_add_f32 v193"))
+    if planted == "dot2c":  # the row-sum test right after the last row-sum dot
+        i = next(i for i, l in enumerate(prog) if l.startswith("v_cmp_ngt_f32"))
         assert prog[i - 1] == "s_nop 2"
         del prog[i - 1]
     elif planted == "exp":  # a P conversion right after the exponential it reads
@@ -261,12 +261,67 @@ def test_loop_registers_stay_in_its_operands_and_clobbers(loop):
     assert {f"v{r}" for r in g.CLOBBERED} <= used
 
 
+def _hd128_refits(prog):
+    """Split the dense head_dim-128 loop into its main path and its out-of-line refit blocks
+    (from an L_refit_ label to the branch back)."""
+    main, refits, cur = [], [], None
+    for l in prog:
+        if l.startswith("L_refit_"):
+            cur = [l]
+        elif cur is not None:
+            cur.append(l)
+            if l.startswith("s_branch L_refitted_"):
+                refits.append(cur)
+                cur = None
+        else:
+            main.append(l)
+    return main, refits
+
+
 def test_loop_covers_four_epochs_of_32_mfmas():
     # the dense loop computes S(1) and copies V(2) before the loop
-    for prog, extra in ((gen.one_phase_program(), 0), (gen.program(), 1)):
+    for prog, extra in ((gen.one_phase_program(), 0), (_hd128_refits(gen.program())[0], 1)):
         assert sum(1 for l in prog if l.startswith("v_mfma")) == 4 * 32 + 16 * extra
         assert sum(1 for l in prog if l == "s_barrier") == 4 + extra
         assert sum(1 for l in prog if l.startswith("global_load_lds")) == 4 * 4 + 2 * extra
+
+
+def test_dense_loop_takes_the_row_max_only_in_its_refits():
+    """The dense head_dim-128 loop's main path has no row max: after each iteration's row sums
+    a lane-partial sum of 128 or more (or NaN) branches to that iteration's refit block, which
+    recomputes S(e) (16 MFMAs from the K slot before krd) and its row max, applies the compiled
+    epoch's lazy rescale (m_tile > m_run + 8 on any lane: m_run, l_run and the 64 O registers
+    updated), recomputes P(e) and its row sums with the main path's own instruction sequence,
+    recomputes S(e+1) (16 MFMAs from krd) and re-issues the next iteration's first V reads; it
+    touches no memory but LDS."""
+    main, refits = _hd128_refits(gen.program())
+    assert len(refits) == 4
+    assert not any(l.startswith(("v_max", "v_permlane")) for l in main)
+    tests = [i for i, l in enumerate(main) if l.startswith("v_cmp_ngt_f32")]
+    assert [main[i] for i in tests] == [f"v_cmp_ngt_f32 vcc, 0x43000000, v{gen.LS}"] * 4
+    for u, r in enumerate(refits):
+        X = gen.P[1] if u % 2 == 0 else gen.P[0]
+        it = gen.spread_iteration(u)
+        assert r[0] == f"L_refit_{u}_%=:" and f"s_cbranch_vccnz L_refit_{u}_%=" in it
+        assert not any(l.startswith(("global_", "buffer_", "scratch_", "s_store", "s_load")) for l in r)
+        mf = [l for l in r if l.startswith("v_mfma")]
+        assert len(mf) == 32
+        dsts = [l.split()[1].rstrip(",") for l in mf]
+        sb1 = f"v[{gen.SB1}:{gen.SB1 + 15}]"
+        assert dsts[:16] == [f"v[{X}:{X + 15}]"] * 8 + [sb1] * 8
+        Y = gen.P[0] if u % 2 == 0 else gen.P[1]
+        assert dsts[16:] == [f"v[{Y}:{Y + 15}]"] * 8 + [sb1] * 8
+        # rescale test and update as the compiled epoch: m_run + 8, any lane, then m_new
+        i = r.index(f"v_add_f32 v{gen.TMP}, 0x41000000, v{gen.MR}")
+        assert r[i + 1:i + 4] == [f"v_cmp_gt_f32 vcc, v{gen.MX}, v{gen.TMP}", "s_nop 3",
+                                  f"s_cbranch_vccz L_kept_{u}_%="]
+        kept = r.index(f"L_kept_{u}_%=:")
+        o_muls = [l for l in r[i:kept] if l.startswith("v_mul_f32 v") and 64 <= int(l.split()[1][1:-1]) < 128]
+        assert len(o_muls) == 64
+        # P(e) and its row sums: the main path's exponential and row-sum instructions, in order
+        p_ops = ("v_fma_f32", "v_exp_f32", "v_cvt_pk_f16_f32", "v_dot2c_f32_f16")
+        assert [l for l in r[kept:] if l.startswith(p_ops)] == [l for l in it if l.startswith(p_ops)]
+        assert r[-1] == f"s_branch L_refitted_{u}_%="
 
 
 def _slots(iteration: list[str]) -> list[list[str]]:

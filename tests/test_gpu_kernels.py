@@ -467,8 +467,9 @@ def test_flash_attention_large_logits(hd):
 def test_flash_attention_scores_rising_along_keys(hd, slope):
     """Scores that rise by `slope` (in log2 units) per 64-key tile along the keys, for every
     query row: the running max must move on most tiles (24: every tile's exponentials
-    against the old reference overflow fp16, so the steps that rescale only on overflow
-    redo P on every tile; 6: every third tile or so).  Against the reference, and the
+    against the old reference overflow fp16, so the head_dim-64 steps that rescale only on
+    overflow and the head_dim-128 loop epochs that take the row max only when a row sum
+    reaches 128 redo P on every tile; 6: every third tile or so).  Against the reference, and the
     generated loops against the compiled steps bit for bit (K/V rows 4 MiB apart, as in
     test_flash_attention_epoch_loop_is_bit_identical)."""
     b, h, s = 1, 2, 1024

@@ -22,8 +22,9 @@ Epoch e of the pair body (key tile e = keys 64e .. 64e+63) does, for every wave:
   rescale   O *= alpha when the rescale ran
   end       wait for the previous epoch's copies, barrier
 
-Each lane performs the same operations on the same operands in the same order as the compiled
-epoch, so the results are bit-identical to it.  The loop covers the epochs [1, 1 + 4*groups),
+Each lane computes every value the compiled epoch keeps (P, m, l, O) with the same operations on
+the same operands in the same order, so the results are bit-identical to it (the dense loop
+computes the row max only when it can matter, below).  The loop covers the epochs [1, 1 + 4*groups),
 which the host side chooses so that no key tile in them needs a causal or length mask (every key
 is below every query row of the workgroup) and no copy is clamped to the last tile.  Without a
 key mask m_run is finite there (epoch 0 saw key 0).  With one, every row of the workgroup has
@@ -34,17 +35,24 @@ one select on that rare path), so l and O cannot turn into NaN if the loop's gat
 rows with different key histories.
 
 The key-masked loop (one_phase_program) runs each epoch in that order.  The dense loop
-(program_spread) computes the same operations per lane in the same order, but software-pipelined
-so that every one of an iteration's 32 MFMA slots carries a share of the softmax: iteration e
-runs the P.V MFMAs of epoch e (slots 0..15) and the score MFMAs of epoch e+1 (key block 0 in
-slots 16..23, key block 1 in 24..31); between them the row max and rescale test of S(e)
-(slots 0..2), the 16 exponential pairs of S(e), computed in place on the score registers
-(slots 3..23), and the row sums in pair order plus the key-block-0 max of S(e+1) (24..31).  The
-scores of epoch 1 are computed before the loop; the last iteration also computes the scores of
-the epoch after the loop, which the compiled epoch recomputes (16 MFMAs per loop).  Two waves of
-a SIMD issuing MFMAs with at most about three VALU instructions and one exponential between
-each pair run at the MFMA rate; the one-phase epoch, with its 32 exponentials between 16 of its
-MFMAs and none between the other 16, cannot hide them.
+(program_spread) computes the same values per lane, but software-pipelined so that every one of
+an iteration's 32 MFMA slots carries a share of the softmax: iteration e runs the P.V MFMAs of
+epoch e (slots 0..15) and the score MFMAs of epoch e+1 (key block 0 in slots 16..23, key block 1
+in 24..31); between them the 16 exponential pairs of S(e), computed in place on the score
+registers (slots 0..23), and the row sums in pair order (24..31).  It skips the row max: the
+exponentials use m_run as it stands, which is what the compiled epoch does whenever its lazy
+rescale does not fire (m_tile <= m_run + 8 on every lane).  When it fires, some P entry is
+exp2(m_tile - m_run) > 2^8 against m_run, so that lane's row sum is at least 256; a row sum of
+128 or more on any lane (or inf / NaN) therefore sends the wave to the iteration's refit block,
+which recomputes S(e), takes its row max and applies the compiled epoch's rescale test and
+update, and recomputes P(e), its row sums and S(e+1) -- the outputs stay bit-identical to the
+compiled epochs, and the row max costs nothing while no row max moves by more than a few
+units (C4: 1070-1072 -> 1037-1038 us against the loop with the max in slots 0..2, same box).  The scores of epoch 1
+are computed before the loop; the last iteration also computes the scores of the epoch after the
+loop, which the compiled epoch recomputes (16 MFMAs per loop).  Two waves of a SIMD issuing
+MFMAs with at most about three VALU instructions and one exponential between each pair run at
+the MFMA rate; the one-phase epoch, with its 32 exponentials between 16 of its MFMAs and none
+between the other 16, cannot hide them.
 
 One loop iteration is 4 epochs, so epoch e = 1 + 4i + u (loop position u) reads V(e-1) from
 V slot (e-1) % 4 = u and writes V(e+1) into slot (u + 2) % 4: both are immediate LDS offsets.
@@ -64,7 +72,8 @@ Register map (all VGPRs; the asm statement pins or clobbers every one of them)
   v[176:191]  P tile region B                     (clobbered)
   v192, v193  m_run, l_run                        (in/out)
   v194..v197  T0, T1, ALPHA, LS (row-sum partial) (clobbered); MX = T0 and TMP = T1 (the S and
-              max phases use MX/TMP, the P.V phase T0/T1)
+              max phases use MX/TMP, the P.V phase T0/T1; the dense loop uses them, and
+              ALPHA, only in its refit blocks)
   v[198:213]  scores, key block 1                 (clobbered)
   v[214:225]  operand ring, 3 x 4: K fragments in the S phase, V fragments in the P.V phase
   v[226:227]  second temporary pair of the exponential pipeline (clobbered); in the dense loop
@@ -118,6 +127,7 @@ S_KB = (92, 93)       # key-validity bits of the tile: lanes' keys 0..31, 32..63
 S_NOKEY = 94          # s[94:95]: lanes whose m_run is still -inf (no valid key yet)
 S_CLOBBERED = list(range(88, 96))
 NEG_INF = "0xff800000"
+P_CHECK = "0x43000000"  # 128.0f: the row-sum level that sends a wave to the exact row max
 
 
 def key_mask(sr, neg: int = ALPHA) -> list[str]:
@@ -311,13 +321,14 @@ def spread_iteration(u: int) -> list[str]:
 
     MFMA slots 0..15: O^T += V^T(e-1) P^T(e-1) (head-dim block c & 3, P block c >> 2);
     slots 16..23: S^T(e+1) key block 0 (k-steps 0..7), slots 24..31: key block 1 (k-steps 0..7).
-    VALU work between them: the key-block-1 half of the row max of S(e), the lane-pair max and
-    the rescale test (slots 0..2; the key-block-0 half ran in slots 26..31 of the iteration
-    before); the 16 exponential pairs of S(e), each computed in place on its two score
-    registers and packed into P register j (slots 3..23: the pairs of key block 1 read SB1,
-    which the key-block-1 MFMAs of S(e+1) overwrite from slot 24, and pair j's pack overwrites
-    the score register of pair j // 2, so the pairs run in order); the fp16 row sums in pair
-    order and the key-block-0 max of S(e+1) (slots 24..31).
+    VALU work between them: the 16 exponential pairs of S(e) against the running reference
+    m_run (no row max), each computed in place on its two score registers and packed into P
+    register j (slots 0..23: the pairs of key block 1 read SB1, which the key-block-1 MFMAs of
+    S(e+1) overwrite from slot 24, and pair j's pack overwrites the score register of pair
+    j // 2, so the pairs run in order); the fp16 row sums in pair order (slots 24..31).  Then
+    the row-sum test: a lane-partial row sum of 128 or more (or inf / NaN) sends the wave to
+    the iteration's refit block (spread_refit), which returns with P(e), its row sums and
+    S(e+1) as the compiled epoch has them.
     """
     X, Y = (P[1], P[0]) if u % 2 == 0 else (P[0], P[1])  # X: S(e) key block 0 -> P(e); Y: P(e-1)
     KB, KA = TX + 1, TX  # K read base (krd + kl0) and the XOR-swizzled address of one k-step
@@ -355,42 +366,10 @@ def spread_iteration(u: int) -> list[str]:
         return f"v_mfma_f32_32x32x16_f16 {v(dst, 16)}, {v(ring(s), 4)}, {v(Q + 4 * kk, 4)}, {src_c}"
 
     slots: list[list[str]] = [[] for _ in range(32)]
-    # ---- row max of S(e): MX holds key block 0's; key block 1's, the lane pair, rescale test ----
-    mx = [f"v_max3_f32 {v(TMP)}, {v(sr(16))}, {v(sr(17))}, {v(sr(18))}"]
-    mx += [f"v_max3_f32 {v(TMP)}, {v(TMP)}, {v(sr(16 + k))}, {v(sr(17 + k))}" for k in range(3, 15, 2)]
-    mx += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(sr(31))}, {v(TMP)}",
-           f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1", f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
-           f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
-           f"v_mul_f32 {v(MX)}, %[cs], {v(MX)}",                 # m_tile
-           f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",            # m_run + 8
-           f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
-           f"s_cbranch_vccnz L_rescale_{u}_%=", f"L_rescaled_{u}_%=:"]
-    for k in range(3):
-        slots[k] += mx[len(mx) * k // 3:len(mx) * (k + 1) // 3]
-
     # ---- exponential pairs, in place: s -> s * cs - m_run -> exp2 -> fp16 pair in P register j ----
-    def scale(j: int) -> list[str]:
-        return [f"v_fma_f32 {v(sr(i))}, {v(sr(i))}, %[cs], -{v(MR)}" for i in (2 * j, 2 * j + 1)]
-
-    def expo(j: int) -> list[str]:
-        return [f"v_exp_f32 {v(sr(i))}, {v(sr(i))}" for i in (2 * j, 2 * j + 1)]
-
-    def pack(j: int) -> list[str]:
-        # P register j = score register j, whose pair (j // 2) is done: pairs run in order
-        return [f"v_cvt_pk_f16_f32 {v(X + j)}, {v(sr(2 * j))}, {v(sr(2 * j + 1))}"]
-
-    stream = []
-    for t in range(18):  # pair t scaled, pair t-1 exponentiated, pair t-2 packed
-        if t < 16:
-            stream += scale(t)
-        if 0 <= t - 1 < 16:
-            stream += expo(t - 1)
-        if 0 <= t - 2 < 16:
-            stream += pack(t - 2)
-    _spread(stream, slots, 3, 23)
-    # ---- fp16 row sums (dot2 with 1.0h) in pair order 0..15; key block 0's max of S(e+1) ----
-    _spread([f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(X + j)}" for j in range(16)], slots, 24, 31)
-    _spread(block0_max(Y), slots, 26, 31)
+    _spread(exp_stream(X), slots, 0, 23)
+    # ---- fp16 row sums (dot2 with 1.0h) in pair order 0..15 ----
+    _spread(row_sums(X), slots, 24, 31)
     # ---- copies: K(e+2) into the K slot kwr (before the iteration's vmcnt), V(e+2) into V slot
     # (u + 3) % 4 (it held V(e-2), last read in the iteration before); the K read base ----
     vw = (3 + (u + 3) % 4) * TILE
@@ -405,7 +384,7 @@ def spread_iteration(u: int) -> list[str]:
     slots[11] += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]
 
     # the reads of slots 0 and 1 were issued by the iteration before (or the scores of epoch 1)
-    L = ["s_mov_b32 %[flag], 0", f"v_mov_b32 {v(LS)}, 0"]
+    L = [f"v_mov_b32 {v(LS)}, 0"]
     issued = [0, 0, 1, 1]  # slot of every LDS read in flight, in issue order
     for s in range(32):
         if s + 2 < 32:
@@ -419,8 +398,10 @@ def spread_iteration(u: int) -> list[str]:
             L += read(s + 2)
             issued += [s + 2] * 2
         L += slots[s]
-    L += ["s_nop 2", f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
-    L += ["s_cmp_lg_u32 %[flag], 0", f"s_cbranch_scc1 L_oscale_{u}_%=", f"L_oscaled_{u}_%=:"]
+    # ---- overflow test on the lane-partial row sums (any lane), then l_run += row sum ----
+    L += ["s_nop 2", f"v_cmp_ngt_f32 vcc, {P_CHECK}, {v(LS)}", "s_nop 3",
+          f"s_cbranch_vccnz L_refit_{u}_%=", f"L_refitted_{u}_%=:",
+          f"v_add_f32 {v(LR)}, {v(LR)}, {v(LS)}"]
     # ---- end: K(e+2) has landed (the V copies may stay in flight), barrier ----
     L += ["s_waitcnt vmcnt(2)", "s_barrier",
           "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
@@ -428,20 +409,94 @@ def spread_iteration(u: int) -> list[str]:
     return L
 
 
-def spread_out_of_line(u: int) -> list[str]:
-    """The rare paths of iteration u, placed after the loop: the lazy rescale and O *= alpha."""
-    L = [f"L_rescale_{u}_%=:",
-         f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",               # m_new
-         f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
-         f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
-         f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",              # m_new = -inf: alpha = 1
-         f"v_mov_b32 {v(MR)}, {v(TMP)}",
-         f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
-         f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}",
-         "s_mov_b32 %[flag], 1", f"s_branch L_rescaled_{u}_%="]
-    L += [f"L_oscale_{u}_%=:"]
+def exp_stream(x: int) -> list[str]:
+    """The 16 exponential pairs of the scores in x (key block 0, entries 0..15) and SB1 (key
+    block 1), in place: s -> s * cs - m_run -> exp2 -> fp16 pair in P register x + j.  Pair t
+    is scaled, pair t-1 exponentiated and pair t-2 packed in turn, so two instructions
+    separate each exponential from the pack that reads it; P register j is score register j,
+    whose pair (j // 2) is done, so the pairs run in order."""
+    def sr(i: int) -> int:
+        return x + i if i < 16 else SB1 + (i - 16)
+
+    stream = []
+    for t in range(18):
+        if t < 16:
+            stream += [f"v_fma_f32 {v(sr(i))}, {v(sr(i))}, %[cs], -{v(MR)}" for i in (2 * t, 2 * t + 1)]
+        if 0 <= t - 1 < 16:
+            stream += [f"v_exp_f32 {v(sr(i))}, {v(sr(i))}" for i in (2 * t - 2, 2 * t - 1)]
+        if 0 <= t - 2 < 16:
+            j = t - 2
+            stream += [f"v_cvt_pk_f16_f32 {v(x + j)}, {v(sr(2 * j))}, {v(sr(2 * j + 1))}"]
+    return stream
+
+
+def row_sums(x: int) -> list[str]:
+    """The lane-partial fp16 row sum of P (registers x .. x+15) into LS, pairs in order 0..15."""
+    return [f"v_dot2c_f32_f16 {v(LS)}, 0x3c003c00, {v(x + j)}" for j in range(16)]
+
+
+def scores_sequential(kb: str, dst: tuple[int, int]) -> list[str]:
+    """S^T of the K tile whose read base (slot + kl0) is in register kb: key block 0 into dst[0],
+    key block 1 into dst[1], one fragment read and one MFMA at a time (the rare refit path)."""
+    KA = TX
+    L = []
+    for f in range(16):
+        blk, kk = f >> 3, f & 7
+        addr = kb
+        if kk:
+            L.append(f"v_xor_b32 {v(KA)}, {kk << 5}, {kb}")
+            addr = v(KA)
+        L += [f"ds_read_b128 {v(RING + 4 * (f % 3), 4)}, {addr} offset:{blk * 8192}", "s_waitcnt lgkmcnt(0)"]
+        src_c = "0" if kk == 0 else v(dst[blk], 16)
+        L.append(f"v_mfma_f32_32x32x16_f16 {v(dst[blk], 16)}, {v(RING + 4 * (f % 3), 4)}, "
+                 f"{v(Q + 4 * kk, 4)}, {src_c}")
+    return L
+
+
+def spread_refit(u: int) -> list[str]:
+    """The refit block of iteration u, placed after the loop: a lane's row sum of P(e) reached
+    128, so the compiled epoch's lazy rescale may fire.  S(e) is recomputed from K(e) (its K
+    slot is the one before krd; it is refilled only after the iteration's barrier) into X and
+    SB1; the row max over the lane pair gives m_tile, and when any lane has m_tile > m_run + 8
+    the compiled epoch's update follows: m_new = max(m_run, m_tile), alpha = exp2(m_run - m_new)
+    (1 when m_new = -inf), l_run and O (which holds the tiles before e) scaled by alpha.  P(e)
+    and its row sums are recomputed in the main path's order (unchanged values when the rescale
+    did not fire); S(e+1) (overwritten) is recomputed from K(e+1) into Y and SB1, and the two V
+    fragment reads the next iteration starts with are issued again."""
+    X, Y = (P[1], P[0]) if u % 2 == 0 else (P[0], P[1])
+    KB = TX + 1
+    L = [f"L_refit_{u}_%=:", "s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7", "s_nop 7",
+         "s_cmp_eq_u32 %[krd], 0", "s_cselect_b32 %[flag], 49152, %[krd]",
+         "s_sub_u32 %[flag], %[flag], 16384",                  # K(e)'s slot
+         f"v_add_u32 {v(KB)}, %[flag], %[kl0]"]
+    L += scores_sequential(v(KB), (X, SB1))
+    L += ["s_nop 7", "s_nop 7", "s_nop 7"]
+    # row max of S(e): key block 0 into MX, key block 1 into TMP, then the lane pair
+    L += block0_max(X)
+    L += [f"v_max3_f32 {v(TMP)}, {v(SB1)}, {v(SB1 + 1)}, {v(SB1 + 2)}"]
+    L += [f"v_max3_f32 {v(TMP)}, {v(TMP)}, {v(SB1 + k)}, {v(SB1 + k + 1)}" for k in range(3, 15, 2)]
+    L += [f"v_max3_f32 {v(MX)}, {v(MX)}, {v(SB1 + 15)}, {v(TMP)}",
+          f"v_mov_b32 {v(TMP)}, {v(MX)}", "s_nop 1", f"v_permlane32_swap_b32 {v(MX)}, {v(TMP)}",
+          f"v_max_f32 {v(MX)}, {v(MX)}, {v(TMP)}",
+          f"v_mul_f32 {v(MX)}, %[cs], {v(MX)}",                 # m_tile
+          f"v_add_f32 {v(TMP)}, 0x41000000, {v(MR)}",            # m_run + 8
+          f"v_cmp_gt_f32 vcc, {v(MX)}, {v(TMP)}", "s_nop 3",
+          f"s_cbranch_vccz L_kept_{u}_%=",
+          f"v_max_f32 {v(TMP)}, {v(MR)}, {v(MX)}",               # m_new
+          f"v_sub_f32 {v(ALPHA)}, {v(MR)}, {v(TMP)}",
+          f"v_exp_f32 {v(ALPHA)}, {v(ALPHA)}",
+          f"v_cmp_eq_f32 vcc, {NEG_INF}, {v(TMP)}",              # m_new = -inf: alpha = 1
+          f"v_mov_b32 {v(MR)}, {v(TMP)}",
+          f"v_cndmask_b32 {v(ALPHA)}, {v(ALPHA)}, 1.0, vcc",
+          f"v_mul_f32 {v(LR)}, {v(LR)}, {v(ALPHA)}"]
     L += [f"v_mul_f32 {v(O + r)}, {v(O + r)}, {v(ALPHA)}" for r in range(64)]
-    L += [f"s_branch L_oscaled_{u}_%="]
+    L += [f"L_kept_{u}_%=:"]
+    L += [f"v_mov_b32 {v(LS)}, 0"] + exp_stream(X) + row_sums(X) + ["s_nop 2"]
+    L += [f"v_add_u32 {v(KB)}, %[krd], %[kl0]"]              # K(e+1)'s slot
+    L += scores_sequential(v(KB), (Y, SB1))
+    L += ["s_nop 7", "s_nop 7", "s_nop 7"]
+    L += vread(0, (u + 1) % 4) + vread(1, (u + 1) % 4)
+    L += [f"s_branch L_refitted_{u}_%="]
     return L
 
 
@@ -479,14 +534,14 @@ def program_spread() -> list[str]:
     L += ["s_waitcnt vmcnt(2)", "s_barrier",
           "s_add_u32 %[krd], %[krd], 16384", "s_cmp_eq_u32 %[krd], 49152", "s_cselect_b32 %[krd], 0, %[krd]",
           "s_nop 7", "s_nop 7", "s_nop 7"]
-    L += block0_max(P[1]) + vread(0, 0) + vread(1, 0)
+    L += vread(0, 0) + vread(1, 0)
     L += ["L_epochs_%=:"]
     for u in range(4):
         L += spread_iteration(u)
     L += ["s_sub_u32 %[cnt], %[cnt], 1", "s_cmp_lg_u32 %[cnt], 0", "s_cbranch_scc1 L_epochs_%=",
           "s_branch L_done_%="]
     for u in range(4):
-        L += spread_out_of_line(u)
+        L += spread_refit(u)
     # the compiled code after the statement reads O and reuses the score registers: MFMA
     # result latency first
     # (and the last iteration's two V reads for an iteration that does not come have landed)
