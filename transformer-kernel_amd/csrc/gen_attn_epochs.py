@@ -39,7 +39,7 @@ The key-masked loop (one_phase_program) runs each epoch in that order.  The dens
 an iteration's 32 MFMA slots carries a share of the softmax: iteration e runs the P.V MFMAs of
 epoch e (slots 0..15) and the score MFMAs of epoch e+1 (key block 0 in slots 16..23, key block 1
 in 24..31); between them the 16 exponential pairs of S(e), computed in place on the score
-registers (slots 0..23), and the row sums in pair order (24..31).  It skips the row max: the
+registers (slots 1..23), and the row sums in pair order (24..31).  It skips the row max: the
 exponentials use m_run as it stands, which is what the compiled epoch does whenever its lazy
 rescale does not fire (m_tile <= m_run + 8 on every lane).  When it fires, some P entry is
 exp2(m_tile - m_run) > 2^8 against m_run, so that lane's row sum is at least 256; a row sum of
@@ -323,7 +323,7 @@ def spread_iteration(u: int) -> list[str]:
     slots 16..23: S^T(e+1) key block 0 (k-steps 0..7), slots 24..31: key block 1 (k-steps 0..7).
     VALU work between them: the 16 exponential pairs of S(e) against the running reference
     m_run (no row max), each computed in place on its two score registers and packed into P
-    register j (slots 0..23: the pairs of key block 1 read SB1, which the key-block-1 MFMAs of
+    register j (slots 1..23: the pairs of key block 1 read SB1, which the key-block-1 MFMAs of
     S(e+1) overwrite from slot 24, and pair j's pack overwrites the score register of pair
     j // 2, so the pairs run in order); the fp16 row sums in pair order (slots 24..31).  Then
     the row-sum test: a lane-partial row sum of 128 or more (or inf / NaN) sends the wave to
@@ -367,7 +367,7 @@ def spread_iteration(u: int) -> list[str]:
 
     slots: list[list[str]] = [[] for _ in range(32)]
     # ---- exponential pairs, in place: s -> s * cs - m_run -> exp2 -> fp16 pair in P register j ----
-    _spread(exp_stream(X), slots, 0, 23)
+    _spread(exp_stream(X), slots, 1, 23)  # slot 0 holds a K copy (0..23: 0.2-0.6 % slower)
     # ---- fp16 row sums (dot2 with 1.0h) in pair order 0..15 ----
     _spread(row_sums(X), slots, 24, 31)
     # ---- copies: K(e+2) into the K slot kwr (before the iteration's vmcnt), V(e+2) into V slot
